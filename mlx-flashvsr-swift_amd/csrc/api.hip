@@ -1,0 +1,525 @@
+// extern "C" entry points of libfvsr_lcsa (declared in include/fvsr_lcsa.h).
+//
+// Host-side responsibilities: argument validation before any device work (the reference traps on the same shape
+// preconditions, SparseAttention.swift:173; DiT.swift:166,297), the context workspace, the KV-ring bookkeeping
+// (slot head / count per layer, the trim rule of DiT.swift:532-538) and kernel launches on the caller's stream.
+// No entry point synchronises the host with the device.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "common.hpp"
+
+namespace fvsr {
+
+static thread_local std::string g_last_error;
+
+int set_error(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+// kernels (lcsa_attn.hip, lcsa_select.hip, kv_ring.hip)
+int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t stream);
+int launch_lists_from_mask(const float* mask, int rows, int nk, int32_t* kidx, int32_t* kcnt, uint8_t* sel,
+                           hipStream_t stream);
+int launch_sel_from_lists(const int32_t* kidx, const int32_t* kcnt, int rows, int nk_stride, int nk, uint8_t* sel,
+                          hipStream_t stream);
+int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, hipStream_t stream);
+int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
+                          const uint8_t* local, float* probs, hipStream_t stream);
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, float* mask_out,
+                     uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
+int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
+                       int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
+                       hipStream_t stream);
+int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,
+                     KeyMap map, hipStream_t stream);
+int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int w, int C, bool to_windows,
+                         hipStream_t stream);
+
+constexpr int kMaxSelectKeyBlocks = 1920;    // scores stage keeps (8 x (128 + Nk)) fp32 in 64 KB of LDS
+constexpr double kAutoThreshold = 0.45;      // DiT.swift:210
+
+static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// workspace carve for one select + attention call
+struct Carve {
+  size_t pq, pk, probs, kidx, kcnt, sel, total;
+};
+static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
+  Carve c;
+  size_t off = 0;
+  c.pq = off; off += align256((size_t)nq * C * 4);
+  c.pk = off; off += align256((size_t)nk * C * 4);
+  c.probs = off; off += align256((size_t)heads * nq * nk * 4);
+  c.kidx = off; off += align256((size_t)heads * nq * nk * 4);
+  c.kcnt = off; off += align256((size_t)heads * nq * 4);
+  c.sel = off; off += align256((size_t)heads * nq * nk);
+  c.total = off;
+  return c;
+}
+
+static bool valid_dtype(int d) { return d == FVSR_DTYPE_F32 || d == FVSR_DTYPE_BF16; }
+static int esize(int d) { return d == FVSR_DTYPE_BF16 ? 2 : 4; }
+
+}  // namespace fvsr
+
+using namespace fvsr;
+
+struct fvsr_ctx {
+  int device = 0;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+struct fvsr_kv_ring {
+  fvsr_ctx* ctx = nullptr;
+  int dtype = 0, layers = 0, heads = 0, bh = 0, bw = 0, s = 0, capacity = 0, kv_len = 0, C = 0;
+  std::vector<int> head, count;
+  void* k = nullptr;         // (layers, capacity * s * 128, C)
+  void* v = nullptr;
+  float* pooled = nullptr;   // (layers, capacity * s, C)
+  size_t layer_tokens() const { return (size_t)capacity * s * kBlock; }
+  char* layer_k(int l) const { return (char*)k + (size_t)l * layer_tokens() * C * esize(dtype); }
+  char* layer_v(int l) const { return (char*)v + (size_t)l * layer_tokens() * C * esize(dtype); }
+  float* layer_pooled(int l) const { return pooled + (size_t)l * capacity * s * C; }
+  KeyMap map(int l) const { return KeyMap{head[l], capacity, s}; }
+};
+
+#define FVSR_REQUIRE(cond, status, msg) \
+  do {                                  \
+    if (!(cond)) return set_error((status), (msg)); \
+  } while (0)
+
+static int ensure_ws(fvsr_ctx* ctx, size_t bytes) {
+  if (ctx->ws_bytes >= bytes) return FVSR_OK;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if (ctx->ws) FVSR_HIP_CHECK(hipFree(ctx->ws));
+  ctx->ws = nullptr;
+  ctx->ws_bytes = 0;
+  if (hipMalloc(&ctx->ws, bytes) != hipSuccess) {
+    ctx->ws = nullptr;
+    return set_error(FVSR_ERR_OUT_OF_MEMORY, "workspace allocation of " + std::to_string(bytes) + " bytes failed");
+  }
+  ctx->ws_bytes = bytes;
+  return FVSR_OK;
+}
+
+static int check_heads(int heads) {
+  FVSR_REQUIRE(heads > 0 && heads <= 4096, FVSR_ERR_INVALID_ARG, "heads must be in [1, 4096]");
+  return FVSR_OK;
+}
+
+extern "C" {
+
+int fvsr_abi_version(void) { return FVSR_ABI_VERSION; }
+
+const char* fvsr_last_error(void) { return g_last_error.c_str(); }
+
+int fvsr_device_props(int device, int* cu_count, int* xcd_count, size_t* lds_bytes, char* arch, size_t arch_len) {
+  hipDeviceProp_t p;
+  FVSR_HIP_CHECK(hipGetDeviceProperties(&p, device));
+  if (cu_count) *cu_count = p.multiProcessorCount;
+  // gfx950 (MI355X) packs 32 CUs per XCD
+  if (xcd_count) *xcd_count = std::max(1, p.multiProcessorCount / 32);
+  if (lds_bytes) *lds_bytes = p.sharedMemPerBlock;
+  if (arch && arch_len) {
+    std::strncpy(arch, p.gcnArchName, arch_len - 1);
+    arch[arch_len - 1] = 0;
+  }
+  return FVSR_OK;
+}
+
+int fvsr_ctx_create(int device, fvsr_ctx** out) {
+  FVSR_REQUIRE(out != nullptr, FVSR_ERR_INVALID_ARG, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  FVSR_HIP_CHECK(hipGetDeviceCount(&n));
+  FVSR_REQUIRE(device >= 0 && device < n, FVSR_ERR_INVALID_ARG, "no such device");
+  fvsr_ctx* c = new (std::nothrow) fvsr_ctx();
+  FVSR_REQUIRE(c != nullptr, FVSR_ERR_OUT_OF_MEMORY, "context allocation failed");
+  c->device = device;
+  *out = c;
+  return FVSR_OK;
+}
+
+int fvsr_ctx_destroy(fvsr_ctx* ctx) {
+  if (!ctx) return FVSR_OK;
+  if (ctx->ws) {
+    (void)hipSetDevice(ctx->device);
+    (void)hipFree(ctx->ws);
+  }
+  delete ctx;
+  return FVSR_OK;
+}
+
+int fvsr_ctx_reserve(fvsr_ctx* ctx, size_t bytes) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  return ensure_ws(ctx, bytes);
+}
+
+size_t fvsr_ctx_workspace_bytes(const fvsr_ctx* ctx) { return ctx ? ctx->ws_bytes : 0; }
+
+size_t fvsr_workspace_size(int heads, int64_t lq, int64_t lk, int channels) {
+  if (heads <= 0 || lq < 0 || lk < 0 || channels <= 0) return 0;
+  return carve(heads, ceil_div(lq, kBlock), ceil_div(lk, kBlock), channels).total;
+}
+
+int fvsr_local_block_mask(int bh, int bw, int range, uint8_t* out) {
+  FVSR_REQUIRE(out != nullptr, FVSR_ERR_INVALID_ARG, "out is NULL");
+  FVSR_REQUIRE(bh > 0 && bw > 0 && range >= 0, FVSR_ERR_INVALID_ARG, "bh, bw must be > 0 and range >= 0");
+  const int half = range / 2, s = bh * bw;
+  for (int qr = 0; qr < bh; ++qr)
+    for (int qc = 0; qc < bw; ++qc)
+      for (int kr = 0; kr < bh; ++kr)
+        for (int kc = 0; kc < bw; ++kc) {
+          const bool in_row = kr >= qr - half && kr <= qr - half + range - 1;
+          const bool in_col = kc >= qc - half && kc <= qc - half + range - 1;
+          out[(size_t)(qr * bw + qc) * s + kr * bw + kc] = (in_row && in_col) ? 1 : 0;
+        }
+  return FVSR_OK;
+}
+
+int fvsr_attention_mode_auto(int topk, int s, int nk, double threshold, double* expected, int* mode) {
+  FVSR_REQUIRE(s > 0 && nk > 0, FVSR_ERR_INVALID_ARG, "s and nk must be > 0");
+  const double e = std::min(1.0, (double)(topk + 1) / ((double)s * (double)nk));
+  if (expected) *expected = e;
+  if (mode) *mode = e <= threshold ? FVSR_ATTN_KERNEL : FVSR_ATTN_DENSE;
+  return FVSR_OK;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// selection
+// ---------------------------------------------------------------------------------------------------------------
+static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const float* pk_src, bool pk_ready,
+                       const void* kW, int64_t lk, KeyMap kmap, int nk, int heads, int q_slices, int s,
+                       const uint8_t* local, int topk, float* mask_out, float* probs_out, int32_t* kidx,
+                       int32_t* kcnt, uint8_t* sel_out, hipStream_t stream) {
+  const int C = heads * kHeadDim;
+  const int64_t nq = ceil_div(lq, kBlock);
+  FVSR_REQUIRE(nq == (int64_t)q_slices * s, FVSR_ERR_INVALID_ARG,
+               "ceil(lq/128) must equal q_slices * s (query blocks split evenly into temporal slices)");
+  FVSR_REQUIRE(nk > 0 && nk <= kMaxSelectKeyBlocks, FVSR_ERR_UNSUPPORTED,
+               "key blocks must be in [1, " + std::to_string(kMaxSelectKeyBlocks) + "]");
+  FVSR_REQUIRE(topk >= 0, FVSR_ERR_INVALID_ARG, "topk must be >= 0");
+  const Carve cv = carve(heads, nq, nk, C);
+  int rc = ensure_ws(ctx, cv.total);
+  if (rc) return rc;
+  char* ws = (char*)ctx->ws;
+  float* pq = (float*)(ws + cv.pq);
+  float* probs = probs_out ? probs_out : (float*)(ws + cv.probs);
+  uint8_t* sel = sel_out ? sel_out : (uint8_t*)(ws + cv.sel);
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if ((rc = launch_pool(dtype, qW, lq, C, pq, stream))) return rc;
+  const float* pk = pk_src;
+  if (!pk_ready) {
+    float* pkw = (float*)(ws + cv.pk);
+    if ((rc = launch_pool(dtype, kW, lk, C, pkw, stream))) return rc;
+    pk = pkw;
+  }
+  if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, stream))) return rc;
+  return launch_topk_emit(probs, heads, (int)nq, nk, q_slices, topk, mask_out, sel, kidx, kcnt, stream);
+}
+
+int fvsr_lcsa_select(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const void* kW, int64_t lk, int heads,
+                     int q_slices, int s, const uint8_t* local_dev, int topk, float* mask_out, float* probs_out,
+                     int32_t* kidx_out, int32_t* kcnt_out, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  FVSR_REQUIRE(valid_dtype(dtype), FVSR_ERR_INVALID_ARG, "dtype must be FVSR_DTYPE_F32 or FVSR_DTYPE_BF16");
+  int rc = check_heads(heads);
+  if (rc) return rc;
+  FVSR_REQUIRE(qW && kW && local_dev && kidx_out && kcnt_out, FVSR_ERR_INVALID_ARG,
+               "qW, kW, local, kidx and kcnt must be non-NULL");
+  FVSR_REQUIRE(lq > 0 && lk > 0, FVSR_ERR_INVALID_ARG, "lq and lk must be > 0");
+  FVSR_REQUIRE(q_slices > 0 && s > 0, FVSR_ERR_INVALID_ARG, "q_slices and s must be > 0");
+  const int64_t nk = ceil_div(lk, kBlock);
+  FVSR_REQUIRE(nk <= kMaxSelectKeyBlocks, FVSR_ERR_UNSUPPORTED, "too many key blocks for selection");
+  return select_impl(ctx, dtype, qW, lq, nullptr, false, kW, lk, KeyMap{0, 1, 1 << 30}, (int)nk, heads, q_slices,
+                     s, local_dev, topk, mask_out, probs_out, kidx_out, kcnt_out, nullptr, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// attention
+// ---------------------------------------------------------------------------------------------------------------
+static AttnArgs make_args(const void* q, int64_t lq, const void* k, const void* v, int64_t lk, int heads,
+                          const int32_t* kidx, const int32_t* kcnt, const uint8_t* sel, int nk_stride, int nk,
+                          KeyMap map, void* o) {
+  AttnArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  a.lq = lq; a.lk = lk;
+  a.heads = heads; a.ld = heads * kHeadDim;
+  a.kidx = kidx; a.kcnt = kcnt; a.sel = sel;
+  a.nk_stride = nk_stride;
+  a.nq = (int)ceil_div(lq, kBlock);
+  a.nk = nk;
+  a.map = map;
+  a.c = (float)(1.4426950408889634 / std::sqrt((double)kHeadDim));
+  return a;
+}
+
+static int check_attn_common(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
+                             int64_t lk, int heads, void* o) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  FVSR_REQUIRE(valid_dtype(dtype), FVSR_ERR_INVALID_ARG, "dtype must be FVSR_DTYPE_F32 or FVSR_DTYPE_BF16");
+  int rc = check_heads(heads);
+  if (rc) return rc;
+  FVSR_REQUIRE(q && k && v && o, FVSR_ERR_INVALID_ARG, "q, k, v and o must be non-NULL");
+  FVSR_REQUIRE(lq > 0 && lk > 0, FVSR_ERR_INVALID_ARG, "lq and lk must be > 0");
+  FVSR_REQUIRE((int64_t)heads * ceil_div(lq, kBlock) < (int64_t)1 << 31, FVSR_ERR_UNSUPPORTED, "grid too large");
+  return FVSR_OK;
+}
+
+int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
+                        int64_t lk, int heads, const int32_t* kidx, const int32_t* kcnt, int nk_stride, void* o,
+                        void* stream) {
+  int rc = check_attn_common(ctx, dtype, q, lq, k, v, lk, heads, o);
+  if (rc) return rc;
+  FVSR_REQUIRE(kidx && kcnt, FVSR_ERR_INVALID_ARG, "kidx and kcnt must be non-NULL");
+  FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
+  const int nk = (int)ceil_div(lk, kBlock);
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  const AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, KeyMap{0, 1, 1 << 30}, o);
+  return launch_attention(dtype, false, a, (hipStream_t)stream);
+}
+
+int fvsr_lcsa_attention_mask(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
+                             int64_t lk, int heads, const float* block_mask, int mode, void* o, void* stream) {
+  int rc = check_attn_common(ctx, dtype, q, lq, k, v, lk, heads, o);
+  if (rc) return rc;
+  FVSR_REQUIRE(block_mask != nullptr, FVSR_ERR_INVALID_ARG, "block_mask is NULL");
+  FVSR_REQUIRE(mode == FVSR_ATTN_KERNEL || mode == FVSR_ATTN_DENSE, FVSR_ERR_INVALID_ARG,
+               "mode must be FVSR_ATTN_KERNEL or FVSR_ATTN_DENSE (auto needs topk: use fvsr_attention_mode_auto)");
+  const int64_t nq = ceil_div(lq, kBlock), nk = ceil_div(lk, kBlock);
+  const Carve cv = carve(heads, nq, nk, heads * kHeadDim);
+  if ((rc = ensure_ws(ctx, cv.total))) return rc;
+  char* ws = (char*)ctx->ws;
+  int32_t* kidx = (int32_t*)(ws + cv.kidx);
+  int32_t* kcnt = (int32_t*)(ws + cv.kcnt);
+  uint8_t* sel = (uint8_t*)(ws + cv.sel);
+  hipStream_t st = (hipStream_t)stream;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if ((rc = launch_lists_from_mask(block_mask, (int)(heads * nq), (int)nk, kidx, kcnt, sel, st))) return rc;
+  const AttnArgs a =
+      make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, KeyMap{0, 1, 1 << 30}, o);
+  return launch_attention(dtype, mode == FVSR_ATTN_DENSE, a, st);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// window layout
+// ---------------------------------------------------------------------------------------------------------------
+static int window_layout(int dtype, const void* x, void* out, int f, int h, int w, int channels, void* stream,
+                         bool to_windows) {
+  FVSR_REQUIRE(valid_dtype(dtype), FVSR_ERR_INVALID_ARG, "dtype must be FVSR_DTYPE_F32 or FVSR_DTYPE_BF16");
+  FVSR_REQUIRE(x && out, FVSR_ERR_INVALID_ARG, "x and out must be non-NULL");
+  FVSR_REQUIRE(f > 0 && h > 0 && w > 0 && f % 2 == 0 && h % 8 == 0 && w % 8 == 0, FVSR_ERR_INVALID_ARG,
+               "window (2, 8, 8) must tile (f, h, w)");
+  FVSR_REQUIRE(channels > 0 && (channels * esize(dtype)) % 16 == 0, FVSR_ERR_INVALID_ARG,
+               "channels * element size must be a multiple of 16 bytes");
+  return launch_window_layout(dtype, x, out, f, h, w, channels, to_windows, (hipStream_t)stream);
+}
+
+int fvsr_window_partition(int dtype, const void* x, void* out, int f, int h, int w, int channels, void* stream) {
+  return window_layout(dtype, x, out, f, h, w, channels, stream, true);
+}
+
+int fvsr_window_reverse(int dtype, const void* x, void* out, int f, int h, int w, int channels, void* stream) {
+  return window_layout(dtype, x, out, f, h, w, channels, stream, false);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// KV ring
+// ---------------------------------------------------------------------------------------------------------------
+int fvsr_kv_ring_create(fvsr_ctx* ctx, int dtype, int layers, int heads, int bh, int bw, int capacity_slices,
+                        int kv_len, fvsr_kv_ring** out) {
+  FVSR_REQUIRE(out != nullptr, FVSR_ERR_INVALID_ARG, "out is NULL");
+  *out = nullptr;
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  FVSR_REQUIRE(valid_dtype(dtype), FVSR_ERR_INVALID_ARG, "dtype must be FVSR_DTYPE_F32 or FVSR_DTYPE_BF16");
+  int rc = check_heads(heads);
+  if (rc) return rc;
+  FVSR_REQUIRE(layers > 0 && bh > 0 && bw > 0, FVSR_ERR_INVALID_ARG, "layers, bh, bw must be > 0");
+  FVSR_REQUIRE(kv_len > 0 && capacity_slices > kv_len, FVSR_ERR_INVALID_ARG,
+               "need kv_len > 0 and capacity_slices > kv_len (the window is read before the trim)");
+  fvsr_kv_ring* r = new (std::nothrow) fvsr_kv_ring();
+  FVSR_REQUIRE(r != nullptr, FVSR_ERR_OUT_OF_MEMORY, "ring allocation failed");
+  r->ctx = ctx;
+  r->dtype = dtype; r->layers = layers; r->heads = heads; r->bh = bh; r->bw = bw; r->s = bh * bw;
+  r->capacity = capacity_slices; r->kv_len = kv_len; r->C = heads * kHeadDim;
+  r->head.assign(layers, 0);
+  r->count.assign(layers, 0);
+  const size_t kv_bytes = (size_t)layers * r->layer_tokens() * r->C * esize(dtype);
+  const size_t pooled_bytes = (size_t)layers * capacity_slices * r->s * r->C * sizeof(float);
+  if (hipSetDevice(ctx->device) != hipSuccess || hipMalloc(&r->k, kv_bytes) != hipSuccess ||
+      hipMalloc(&r->v, kv_bytes) != hipSuccess || hipMalloc((void**)&r->pooled, pooled_bytes) != hipSuccess) {
+    if (r->k) (void)hipFree(r->k);
+    if (r->v) (void)hipFree(r->v);
+    if (r->pooled) (void)hipFree(r->pooled);
+    delete r;
+    return set_error(FVSR_ERR_OUT_OF_MEMORY, "ring allocation of 2 x " + std::to_string(kv_bytes) + " bytes failed");
+  }
+  *out = r;
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_destroy(fvsr_kv_ring* r) {
+  if (!r) return FVSR_OK;
+  (void)hipSetDevice(r->ctx->device);
+  (void)hipFree(r->k);
+  (void)hipFree(r->v);
+  (void)hipFree(r->pooled);
+  delete r;
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_reset(fvsr_kv_ring* r) {
+  FVSR_REQUIRE(r != nullptr, FVSR_ERR_INVALID_ARG, "ring is NULL");
+  std::fill(r->head.begin(), r->head.end(), 0);
+  std::fill(r->count.begin(), r->count.end(), 0);
+  return FVSR_OK;
+}
+
+static int check_layer(const fvsr_kv_ring* r, int layer) {
+  FVSR_REQUIRE(r != nullptr, FVSR_ERR_INVALID_ARG, "ring is NULL");
+  FVSR_REQUIRE(layer >= 0 && layer < r->layers, FVSR_ERR_INVALID_ARG, "layer out of range");
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_append(fvsr_kv_ring* r, int layer, const void* k_new, const void* v_new, int n_slices, int layout,
+                        void* stream) {
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(k_new && v_new, FVSR_ERR_INVALID_ARG, "k_new and v_new must be non-NULL");
+  FVSR_REQUIRE(n_slices > 0, FVSR_ERR_INVALID_ARG, "n_slices must be > 0");
+  FVSR_REQUIRE(layout == FVSR_LAYOUT_WINDOWS || layout == FVSR_LAYOUT_GRID, FVSR_ERR_INVALID_ARG, "bad layout");
+  FVSR_REQUIRE(r->count[layer] + n_slices <= r->capacity, FVSR_ERR_CAPACITY,
+               "append of " + std::to_string(n_slices) + " slices exceeds the ring capacity of " +
+                   std::to_string(r->capacity) + " (held " + std::to_string(r->count[layer]) + ")");
+  FVSR_HIP_CHECK(hipSetDevice(r->ctx->device));
+  const int slot0 = (r->head[layer] + r->count[layer]) % r->capacity;
+  rc = launch_ring_append(r->dtype, k_new, v_new, n_slices * r->s, r->C, layout == FVSR_LAYOUT_GRID, r->bh, r->bw,
+                          slot0, r->capacity, r->layer_k(layer), r->layer_v(layer), r->layer_pooled(layer),
+                          (hipStream_t)stream);
+  if (rc) return rc;
+  r->count[layer] += n_slices;
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_evict(fvsr_kv_ring* r, int layer) {
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  // DiT.swift:532-538: more than kv_len slices held -> drop exactly one (the oldest)
+  if (r->count[layer] > r->kv_len) {
+    r->head[layer] = (r->head[layer] + 1) % r->capacity;
+    r->count[layer] -= 1;
+  }
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_slices(const fvsr_kv_ring* r, int layer, int* out) {
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(out != nullptr, FVSR_ERR_INVALID_ARG, "out is NULL");
+  *out = r->count[layer];
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_read(fvsr_kv_ring* r, int layer, void* k_out, void* v_out, void* stream) {
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(k_out && v_out, FVSR_ERR_INVALID_ARG, "k_out and v_out must be non-NULL");
+  FVSR_HIP_CHECK(hipSetDevice(r->ctx->device));
+  return launch_ring_read(r->dtype, r->layer_k(layer), r->layer_v(layer), k_out, v_out, r->count[layer] * r->s,
+                          r->C, r->map(layer), (hipStream_t)stream);
+}
+
+int fvsr_lcsa_select_ring(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* qW, int64_t lq, int q_slices,
+                          const uint8_t* local_dev, int topk, float* mask_out, float* probs_out, int32_t* kidx_out,
+                          int32_t* kcnt_out, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(r->count[layer] > 0, FVSR_ERR_STATE, "ring layer holds no keys");
+  FVSR_REQUIRE(qW && local_dev && kidx_out && kcnt_out, FVSR_ERR_INVALID_ARG,
+               "qW, local, kidx and kcnt must be non-NULL");
+  FVSR_REQUIRE(lq > 0 && q_slices > 0, FVSR_ERR_INVALID_ARG, "lq and q_slices must be > 0");
+  const int nk = r->count[layer] * r->s;
+  return select_impl(ctx, r->dtype, qW, lq, r->layer_pooled(layer), true, nullptr, (int64_t)nk * kBlock,
+                     r->map(layer), nk, r->heads, q_slices, r->s, local_dev, topk, mask_out, probs_out, kidx_out,
+                     kcnt_out, nullptr, (hipStream_t)stream);
+}
+
+static int attention_ring_impl(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q, int64_t lq,
+                               const int32_t* kidx, const int32_t* kcnt, int nk_stride, const uint8_t* sel,
+                               bool dense, void* o, hipStream_t stream) {
+  const int nk = r->count[layer] * r->s;
+  const AttnArgs a = make_args(q, lq, r->layer_k(layer), r->layer_v(layer), (int64_t)nk * kBlock, r->heads, kidx,
+                               kcnt, sel, nk_stride, nk, r->map(layer), o);
+  return launch_attention(r->dtype, dense, a, stream);
+}
+
+int fvsr_lcsa_attention_ring(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q, int64_t lq,
+                             const int32_t* kidx, const int32_t* kcnt, int nk_stride, int mode, void* o,
+                             void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(r->count[layer] > 0, FVSR_ERR_STATE, "ring layer holds no keys");
+  FVSR_REQUIRE(q && kidx && kcnt && o, FVSR_ERR_INVALID_ARG, "q, kidx, kcnt and o must be non-NULL");
+  FVSR_REQUIRE(lq > 0 && nk_stride > 0, FVSR_ERR_INVALID_ARG, "lq and nk_stride must be > 0");
+  FVSR_REQUIRE(mode == FVSR_ATTN_KERNEL || mode == FVSR_ATTN_DENSE, FVSR_ERR_INVALID_ARG,
+               "mode must be FVSR_ATTN_KERNEL or FVSR_ATTN_DENSE");
+  hipStream_t st = (hipStream_t)stream;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  const int64_t nq = ceil_div(lq, kBlock);
+  const int nk = r->count[layer] * r->s;
+  uint8_t* sel = nullptr;
+  if (mode == FVSR_ATTN_DENSE) {
+    const Carve cv = carve(r->heads, nq, nk, r->C);
+    if ((rc = ensure_ws(ctx, cv.total))) return rc;
+    sel = (uint8_t*)((char*)ctx->ws + cv.sel);
+    if ((rc = launch_sel_from_lists(kidx, kcnt, (int)(r->heads * nq), nk_stride, nk, sel, st))) return rc;
+  }
+  return attention_ring_impl(ctx, r, layer, q, lq, kidx, kcnt, nk_stride, sel, mode == FVSR_ATTN_DENSE, o, st);
+}
+
+int fvsr_lcsa_layer(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* qW, int64_t lq, const void* k_new,
+                    const void* v_new, int n_new_slices, int layout, int q_slices, const uint8_t* local_dev,
+                    int topk, int mode, void* o, float* mask_out, float* probs_out, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(qW && o && local_dev, FVSR_ERR_INVALID_ARG, "qW, o and local must be non-NULL");
+  FVSR_REQUIRE(mode == FVSR_ATTN_AUTO || mode == FVSR_ATTN_KERNEL || mode == FVSR_ATTN_DENSE,
+               FVSR_ERR_INVALID_ARG, "bad attention mode");
+  FVSR_REQUIRE(lq > 0 && q_slices > 0 && topk >= 0, FVSR_ERR_INVALID_ARG, "lq, q_slices must be > 0, topk >= 0");
+  FVSR_REQUIRE(ceil_div(lq, kBlock) == (int64_t)q_slices * r->s, FVSR_ERR_INVALID_ARG,
+               "ceil(lq/128) must equal q_slices * s");
+  FVSR_REQUIRE(r->count[layer] + n_new_slices <= r->capacity, FVSR_ERR_CAPACITY,
+               "append would exceed the ring capacity");
+  const int nk_after = (r->count[layer] + n_new_slices) * r->s;
+  FVSR_REQUIRE(nk_after <= kMaxSelectKeyBlocks, FVSR_ERR_UNSUPPORTED, "too many key blocks for selection");
+  hipStream_t st = (hipStream_t)stream;
+  // workspace first, so that no allocation happens between the append and the evict
+  const int64_t nq = ceil_div(lq, kBlock);
+  const Carve cv = carve(r->heads, nq, nk_after, r->C);
+  if ((rc = ensure_ws(ctx, cv.total))) return rc;
+  if ((rc = fvsr_kv_ring_append(r, layer, k_new, v_new, n_new_slices, layout, stream))) return rc;
+  const int nk = r->count[layer] * r->s;
+  char* ws = (char*)ctx->ws;
+  int32_t* kidx = (int32_t*)(ws + cv.kidx);
+  int32_t* kcnt = (int32_t*)(ws + cv.kcnt);
+  uint8_t* sel = (uint8_t*)(ws + cv.sel);
+  rc = select_impl(ctx, r->dtype, qW, lq, r->layer_pooled(layer), true, nullptr, (int64_t)nk * kBlock,
+                   r->map(layer), nk, r->heads, q_slices, r->s, local_dev, topk, mask_out, probs_out, kidx, kcnt,
+                   sel, st);
+  if (rc) return rc;
+  int use = mode;
+  if (use == FVSR_ATTN_AUTO) fvsr_attention_mode_auto(topk, r->s, nk, kAutoThreshold, nullptr, &use);
+  rc = attention_ring_impl(ctx, r, layer, qW, lq, kidx, kcnt, nk, sel, use == FVSR_ATTN_DENSE, o, st);
+  if (rc) return rc;
+  return fvsr_kv_ring_evict(r, layer);
+}
+
+}  // extern "C"

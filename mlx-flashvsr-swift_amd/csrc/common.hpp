@@ -1,0 +1,78 @@
+// Shared types and helpers for the gfx950 LCSA kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+#include "../../include/fvsr_lcsa.h"
+
+namespace fvsr {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 128;     // tokens per LCSA window / block
+constexpr int kHeadDim = 128;   // head dim of every FlashVSR head
+constexpr int kXcds = 8;        // MI355X: 8 XCDs, workgroups dispatched round-robin across them
+
+// Records the failure message for fvsr_last_error() and returns the status (defined in api.hip).
+int set_error(int status, const std::string& msg);
+
+#define FVSR_HIP_CHECK(expr)                                                                          \
+  do {                                                                                                \
+    hipError_t e_ = (expr);                                                                           \
+    if (e_ != hipSuccess)                                                                             \
+      return ::fvsr::set_error(FVSR_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_));      \
+  } while (0)
+
+// Workgroups are dispatched round-robin over the XCDs (each with its own L2). Remap so that every XCD owns one
+// contiguous range of logical work items: neighbouring (head, query block) items — which select overlapping key
+// blocks — then share one L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
+  const int xcd = bid % kXcds, idx = bid / kXcds;
+  const int q = nwg / kXcds, rem = nwg % kXcds;
+  return xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
+}
+
+// Logical key block j of the key range -> first token row of that block in the K/V buffer.
+// Plain buffers: (slot_head 0, capacity 1, slice_blocks >= Nk) gives row j*128.
+// Ring: block j lives in slot (head + j / s) % capacity at block j % s of that slot.
+struct KeyMap {
+  int slot_head;
+  int capacity;
+  int slice_blocks;
+  __device__ __forceinline__ int64_t row(int j) const {
+    const int slot = (slot_head + j / slice_blocks) % capacity;
+    return ((int64_t)slot * slice_blocks + (j % slice_blocks)) * kBlock;
+  }
+};
+
+// Arguments of the attention kernels (lcsa_attn.hip).
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t lq;            // valid query tokens
+  int64_t lk;            // valid key tokens (logical key range)
+  int heads;
+  int ld;                // channels per token = heads * 128
+  const int32_t* kidx;   // (H, nq, nk_stride) listed key blocks
+  const int32_t* kcnt;   // (H, nq)
+  const uint8_t* sel;    // (H, nq, nk) selection bytes, dense mode only
+  int nk_stride;
+  int nq;
+  int nk;
+  KeyMap map;
+  float c;               // softmax scale * log2(e)
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace fvsr

@@ -1,0 +1,135 @@
+// Streaming KV window cache (ring) and window-layout kernels for gfx950 (MI355X).
+//
+// Reference semantics: the window K/V cache of `blockForward` (DiT.swift:507-511 concat, :532-538 trim) and
+// `windowPartition` / `windowReverse` (DiT.swift:113-126).
+//
+// Design: the reference rebuilds the whole window each chunk (concat = read cache + new, write all). Here each
+// layer owns `capacity` slots of one temporal slice (s blocks x 128 tokens x C) in window order; an append writes
+// only the new slices into the next free slots (and mean-pools each new key block on the way, so selection never
+// re-reads cached keys); evict moves the ring head. Attention and selection address key block j through
+// slot = (head + j / s) % capacity. All kernels are pure HBM streams: one workgroup per 128-token block, 16-byte
+// loads/stores, 8 tokens in flight per thread.
+#include "common.hpp"
+
+namespace fvsr {
+
+// token t (0..127) of window b -> natural (f, h, w) token index, windows ordered (nf, nh, nw), tokens (wf, wh, ww)
+__device__ __forceinline__ int64_t window_token_to_grid(int b, int t, int nbh, int nbw) {
+  const int per_slice = nbh * nbw;
+  const int nf = b / per_slice, rem = b % per_slice;
+  const int nh = rem / nbw, nw = rem % nbw;
+  const int wf = t >> 6, wh = (t >> 3) & 7, ww = t & 7;
+  const int64_t H = 8 * nbh, W = 8 * nbw;
+  return ((int64_t)(2 * nf + wf) * H + 8 * nh + wh) * W + 8 * nw + ww;
+}
+
+// Copies 128-token blocks between layouts (16 bytes per vector). Block b of the source maps to block dst_block(b)
+// of the destination; tokens inside a block may be gathered from grid order (src_grid) or scattered to grid order
+// (dst_grid). When `pooled` is set, also writes the fp32 mean of each source block (the pooled key).
+template <typename T>
+__global__ void block_copy_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, bool src_grid,
+                                  bool dst_grid, int nbh, int nbw, int dst_slot0, int capacity, int slice_blocks,
+                                  float* __restrict__ pooled, const T* __restrict__ src2, T* __restrict__ dst2) {
+  constexpr int VN = 16 / sizeof(T);
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const int b = blockIdx.x;
+  // destination block: ring slot (dst_slot0 + b / s) % capacity, block b % s; identity when capacity == 1 and
+  // slice_blocks >= the block count
+  const int64_t db = (int64_t)((dst_slot0 + b / slice_blocks) % capacity) * slice_blocks + (b % slice_blocks);
+  const int nvec = C / VN;
+  for (int cv = threadIdx.x; cv < nvec; cv += blockDim.x) {
+    float acc[VN];
+#pragma unroll
+    for (int e = 0; e < VN; ++e) acc[e] = 0.f;
+#pragma unroll 8
+    for (int t = 0; t < kBlock; ++t) {
+      const int64_t si = src_grid ? window_token_to_grid(b, t, nbh, nbw) : (int64_t)b * kBlock + t;
+      const int64_t di = dst_grid ? window_token_to_grid((int)db, t, nbh, nbw) : db * kBlock + t;
+      const u4 x = *(const u4*)(src + si * C + cv * VN);
+      *(u4*)(dst + di * C + cv * VN) = x;
+      if (src2) *(u4*)(dst2 + di * C + cv * VN) = *(const u4*)(src2 + si * C + cv * VN);
+      if (pooled) {
+        const T* xv = (const T*)&x;
+#pragma unroll
+        for (int e = 0; e < VN; ++e) acc[e] += (float)xv[e];
+      }
+    }
+    if (pooled) {
+#pragma unroll
+      for (int e = 0; e < VN; ++e) pooled[db * C + cv * VN + e] = acc[e] / (float)kBlock;
+    }
+  }
+}
+
+// Ring -> window order: logical block j of the held window (slot (head + j/s) % capacity) -> block j of dst.
+template <typename T>
+__global__ void ring_read_kernel(const T* __restrict__ rk, const T* __restrict__ rv, T* __restrict__ ok,
+                                 T* __restrict__ ov, int C, KeyMap map) {
+  constexpr int VN = 16 / sizeof(T);
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const int j = blockIdx.x;
+  const int64_t sr = map.row(j), dr = (int64_t)j * kBlock;
+  const int nvec = C / VN;
+  for (int e = threadIdx.x; e < kBlock * nvec; e += blockDim.x) {
+    const int t = e / nvec, cv = e % nvec;
+    *(u4*)(ok + (dr + t) * C + cv * VN) = *(const u4*)(rk + (sr + t) * C + cv * VN);
+    *(u4*)(ov + (dr + t) * C + cv * VN) = *(const u4*)(rv + (sr + t) * C + cv * VN);
+  }
+}
+
+static int copy_threads(int C, int esize) {
+  const int nvec = C * esize / 16;
+  return std::min(1024, ((nvec + 63) / 64) * 64);
+}
+
+int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
+                       int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
+                       hipStream_t stream) {
+  if (n_blocks <= 0) return FVSR_OK;
+  const int s = nbh * nbw;
+  if (dtype == FVSR_DTYPE_BF16) {
+    hipLaunchKernelGGL(block_copy_kernel<bf16>, dim3(n_blocks), dim3(copy_threads(C, 2)), 0, stream,
+                       (const bf16*)k_new, (bf16*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s,
+                       pooled, (const bf16*)v_new, (bf16*)ring_v);
+  } else {
+    hipLaunchKernelGGL(block_copy_kernel<float>, dim3(n_blocks), dim3(copy_threads(C, 4)), 0, stream,
+                       (const float*)k_new, (float*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s,
+                       pooled, (const float*)v_new, (float*)ring_v);
+  }
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,
+                     KeyMap map, hipStream_t stream) {
+  if (n_blocks <= 0) return FVSR_OK;
+  if (dtype == FVSR_DTYPE_BF16)
+    hipLaunchKernelGGL(ring_read_kernel<bf16>, dim3(n_blocks), dim3(256), 0, stream, (const bf16*)rk,
+                       (const bf16*)rv, (bf16*)ok, (bf16*)ov, C, map);
+  else
+    hipLaunchKernelGGL(ring_read_kernel<float>, dim3(n_blocks), dim3(256), 0, stream, (const float*)rk,
+                       (const float*)rv, (float*)ok, (float*)ov, C, map);
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+// natural (f, h, w) order <-> window order, one workgroup per window
+int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int w, int C, bool to_windows,
+                         hipStream_t stream) {
+  const int nbh = h / 8, nbw = w / 8;
+  const int n_blocks = (f / 2) * nbh * nbw;
+  if (n_blocks <= 0) return FVSR_OK;
+  const int big = 1 << 30;   // identity destination mapping
+  if (dtype == FVSR_DTYPE_BF16)
+    hipLaunchKernelGGL(block_copy_kernel<bf16>, dim3(n_blocks), dim3(copy_threads(C, 2)), 0, stream,
+                       (const bf16*)x, (bf16*)out, C, to_windows, !to_windows, nbh, nbw, 0, 1, big,
+                       (float*)nullptr, (const bf16*)nullptr, (bf16*)nullptr);
+  else
+    hipLaunchKernelGGL(block_copy_kernel<float>, dim3(n_blocks), dim3(copy_threads(C, 4)), 0, stream,
+                       (const float*)x, (float*)out, C, to_windows, !to_windows, nbh, nbw, 0, 1, big,
+                       (float*)nullptr, (const float*)nullptr, (float*)nullptr);
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+}  // namespace fvsr

@@ -1,0 +1,273 @@
+// LCSA block selection for gfx950 (MI355X).
+//
+// Reference semantics: `draftBlockMaskAndProbs` (DiT.swift:158-174) and the kcnt/kidx build of
+// `kernelBlockAttention` (SparseAttention.swift:175-177):
+//   pq, pk = fp32 mean of each 128-token window, per head;
+//   scores = pq . pk^T / sqrt(128) (a true divide), -inf where the local window (tiled over every (query slice,
+//   key slice) pair) hides the key block; probs = softmax over the key blocks;
+//   per (head, query temporal slice) keep the entries STRICTLY above the (k+1)-th largest of the s*Nk probs,
+//   k = min(n - 1, topk).
+//
+// Kernels (all HBM/L2-bound, no MFMA — the score product is 0.1 GFLOP):
+//   pool_kernel          one workgroup per 128-token block: coalesced 16-byte loads, fp32 sums, mean
+//   scores_softmax_kernel one workgroup per (8 query blocks, head): pooled-key rows read once per 8 query rows,
+//                         scores + local mask staged in LDS, one wave per row for max / exp / sum / normalise
+//   topk_emit_kernel     one 1024-thread workgroup per (head, query slice): exact k-th-largest by a 4 x 8-bit
+//                         radix select over the fp32 bit patterns (probs are >= 0, so bit order = value order),
+//                         per-wave LDS histograms; then the mask, selection bytes and compacted key lists
+//                         (ballot + popcount) for every query row of the slice.
+#include "common.hpp"
+
+namespace fvsr {
+
+// ------------------------------------------------------------------------------------------------------------
+// pooling
+// ------------------------------------------------------------------------------------------------------------
+template <typename T>
+struct Vec16;   // 16-byte vector of T
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  typedef f32x4 type;
+};
+template <>
+struct Vec16<bf16> {
+  static constexpr int N = 8;
+  typedef bf16x8 type;
+};
+
+// x: (L, C) tokens; out: (nb, C) fp32 means; block b pools rows [b*128, min(L, b*128+128)).
+template <typename T>
+__global__ void pool_kernel(const T* __restrict__ x, int64_t L, int C, float* __restrict__ out) {
+  constexpr int VN = Vec16<T>::N;
+  typedef typename Vec16<T>::type VT;
+  const int b = blockIdx.x;
+  const int64_t r0 = (int64_t)b * kBlock;
+  const int n = (int)min<int64_t>(kBlock, L - r0);
+  const int nvec = C / VN;
+  for (int cv = threadIdx.x; cv < nvec; cv += blockDim.x) {
+    float acc[VN];
+#pragma unroll
+    for (int e = 0; e < VN; ++e) acc[e] = 0.f;
+    const T* p = x + r0 * C + cv * VN;
+#pragma unroll 8
+    for (int r = 0; r < n; ++r) {
+      const VT v = *(const VT*)(p + (int64_t)r * C);
+#pragma unroll
+      for (int e = 0; e < VN; ++e) acc[e] += (float)v[e];
+    }
+    float* o = out + (int64_t)b * C + cv * VN;
+#pragma unroll
+    for (int e = 0; e < VN; ++e) o[e] = acc[e] / (float)n;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// scores + softmax
+// ------------------------------------------------------------------------------------------------------------
+constexpr int kScoreRows = 8;   // query blocks per workgroup
+
+// pq: (nq, C) pooled queries; pk: pooled keys, logical key block j at row map.row(j)/128 of pk (C floats each);
+// local: (s, s) bytes; probs: (H, nq, nk).
+__global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __restrict__ pq,
+                                                             const float* __restrict__ pk, KeyMap kmap, int C,
+                                                             int nq, int nk, int s,
+                                                             const uint8_t* __restrict__ local,
+                                                             float* __restrict__ probs) {
+  extern __shared__ float sm[];
+  float* qs = sm;                          // [kScoreRows][128]
+  float* ss = sm + kScoreRows * kHeadDim;  // [kScoreRows][nk]
+  const int h = blockIdx.y;
+  const int i0 = blockIdx.x * kScoreRows;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < kScoreRows * kHeadDim; e += blockDim.x) {
+    const int r = e / kHeadDim, d = e % kHeadDim;
+    qs[e] = (i0 + r < nq) ? pq[(int64_t)(i0 + r) * C + h * kHeadDim + d] : 0.f;
+  }
+  __syncthreads();
+  const float sqrt_d = sqrtf((float)kHeadDim);
+#pragma unroll 1
+  for (int j = tid; j < nk; j += blockDim.x) {
+    // keep the (loop-invariant) pooled-query reads inside the loop: hoisting 8 x 128 floats spills
+    asm volatile("" ::: "memory");
+    const float* krow = pk + (kmap.row(j) / kBlock) * C + h * kHeadDim;
+    float acc[kScoreRows];
+#pragma unroll
+    for (int r = 0; r < kScoreRows; ++r) acc[r] = 0.f;
+#pragma unroll 4
+    for (int d0 = 0; d0 < kHeadDim; d0 += 4) {
+      const f32x4 kv = *(const f32x4*)(krow + d0);
+#pragma unroll
+      for (int r = 0; r < kScoreRows; ++r) {
+        const f32x4 qv = *(const f32x4*)(qs + r * kHeadDim + d0);
+        acc[r] = fmaf(qv[0], kv[0], acc[r]);
+        acc[r] = fmaf(qv[1], kv[1], acc[r]);
+        acc[r] = fmaf(qv[2], kv[2], acc[r]);
+        acc[r] = fmaf(qv[3], kv[3], acc[r]);
+      }
+    }
+    const int ksp = j % s;
+#pragma unroll
+    for (int r = 0; r < kScoreRows; ++r) {
+      const int qsp = (i0 + r) % s;
+      ss[r * nk + j] = local[qsp * s + ksp] ? acc[r] / sqrt_d : -INFINITY;
+    }
+  }
+  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63, nwaves = blockDim.x >> 6;
+  for (int r = wave; r < kScoreRows; r += nwaves) {
+    if (i0 + r >= nq) break;
+    const float* srow = ss + r * nk;
+    float mx = -INFINITY;
+    for (int j = lane; j < nk; j += 64) mx = fmaxf(mx, srow[j]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.f;
+    for (int j = lane; j < nk; j += 64) sum += expf(srow[j] - mx);
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    float* prow = probs + ((int64_t)h * nq + i0 + r) * nk;
+    for (int j = lane; j < nk; j += 64) prow[j] = expf(srow[j] - mx) / sum;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// exact top-k threshold + mask / list emit
+// ------------------------------------------------------------------------------------------------------------
+constexpr int kTopkThreads = 1024;
+
+__global__ __launch_bounds__(kTopkThreads) void topk_emit_kernel(const float* __restrict__ probs, int nq, int nk,
+                                                                 int q_slices, int topk,
+                                                                 float* __restrict__ mask_out,
+                                                                 uint8_t* __restrict__ sel,
+                                                                 int32_t* __restrict__ kidx,
+                                                                 int32_t* __restrict__ kcnt) {
+  __shared__ unsigned hist[kTopkThreads / 64][256];
+  __shared__ unsigned tot[256];
+  __shared__ unsigned s_prefix, s_rank;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row = blockIdx.x;                       // (head, query slice)
+  const int h = row / q_slices, t = row % q_slices;
+  const int sq = nq / q_slices;
+  const int64_t base = ((int64_t)h * nq + (int64_t)t * sq) * nk;
+  const unsigned* bits = (const unsigned*)(probs + base);
+  const int64_t n = (int64_t)sq * nk;
+  const int64_t k = min<int64_t>(n - 1, topk);
+  unsigned rank = (unsigned)(n - 1 - k);            // ascending rank of the (k+1)-th largest
+  unsigned prefix = 0, pmask = 0;
+  if (tid == 0) {
+    s_prefix = 0;
+    s_rank = rank;
+  }
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int e = tid; e < (kTopkThreads / 64) * 256; e += kTopkThreads) (&hist[0][0])[e] = 0;
+    __syncthreads();
+    for (int64_t e = tid; e < n; e += kTopkThreads) {
+      const unsigned u = bits[e];
+      if ((u & pmask) == prefix) atomicAdd(&hist[wave][(u >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 256) {
+      unsigned c = 0;
+#pragma unroll
+      for (int w = 0; w < kTopkThreads / 64; ++w) c += hist[w][tid];
+      tot[tid] = c;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // lane owns bins 4*lane .. 4*lane+3
+      const unsigned c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
+      const unsigned lsum = c0 + c1 + c2 + c3;
+      unsigned incl = lsum;
+      for (int o = 1; o < 64; o <<= 1) {
+        const unsigned y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      const unsigned excl = incl - lsum;
+      if (rank >= excl && rank < incl) {
+        unsigned cum = excl, d = 4 * lane;
+        const unsigned cs[4] = {c0, c1, c2, c3};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (rank < cum + cs[q]) { d = 4 * lane + q; break; }
+          cum += cs[q];
+        }
+        s_prefix = prefix | (d << shift);
+        s_rank = rank - cum;
+      }
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    rank = s_rank;
+    pmask |= 255u << shift;
+  }
+  const float thr = __uint_as_float(prefix);
+
+  // emit for every query row of this slice: one wave per row
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int i = wave; i < sq; i += kTopkThreads / 64) {
+    const int qi = t * sq + i;
+    const int64_t roff = ((int64_t)h * nq + qi) * nk;
+    const float* prow = probs + roff;
+    int32_t* krow = kidx + roff;
+    int n_sel = 0;
+    for (int j0 = 0; j0 < nk; j0 += 64) {
+      const int j = j0 + lane;
+      const bool s = j < nk && prow[j] > thr;
+      const uint64_t b = __ballot(s);
+      if (s) krow[n_sel + __popcll(b & lt)] = j;
+      if (j < nk) {
+        sel[roff + j] = s ? 1 : 0;
+        if (mask_out) mask_out[roff + j] = s ? 1.f : 0.f;
+      }
+      n_sel += __popcll(b);
+    }
+    int n_un = n_sel;
+    for (int j0 = 0; j0 < nk; j0 += 64) {
+      const int j = j0 + lane;
+      const bool u = j < nk && !(prow[j] > thr);
+      const uint64_t b = __ballot(u);
+      if (u) krow[n_un + __popcll(b & lt)] = j;
+      n_un += __popcll(b);
+    }
+    if (lane == 0) kcnt[(int64_t)h * nq + qi] = n_sel;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// launch
+// ------------------------------------------------------------------------------------------------------------
+int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, hipStream_t stream) {
+  const int nb = (int)ceil_div(L, kBlock);
+  if (nb <= 0) return FVSR_OK;
+  const int vn = dtype == FVSR_DTYPE_BF16 ? 8 : 4;
+  const int nvec = C / vn;
+  const int threads = std::min(1024, ((nvec + 63) / 64) * 64);
+  if (dtype == FVSR_DTYPE_BF16)
+    hipLaunchKernelGGL(pool_kernel<bf16>, dim3(nb), dim3(threads), 0, stream, (const bf16*)x, L, C, out);
+  else
+    hipLaunchKernelGGL(pool_kernel<float>, dim3(nb), dim3(threads), 0, stream, (const float*)x, L, C, out);
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+size_t scores_smem_bytes(int nk) { return sizeof(float) * (size_t)kScoreRows * (kHeadDim + nk); }
+
+int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
+                          const uint8_t* local, float* probs, hipStream_t stream) {
+  if (nq <= 0 || nk <= 0) return FVSR_OK;
+  dim3 grid((nq + kScoreRows - 1) / kScoreRows, heads);
+  hipLaunchKernelGGL(scores_softmax_kernel, grid, dim3(256), scores_smem_bytes(nk), stream, pq, pk, kmap, C, nq,
+                     nk, s, local, probs);
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, float* mask_out,
+                     uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream) {
+  if (nq <= 0 || nk <= 0) return FVSR_OK;
+  hipLaunchKernelGGL(topk_emit_kernel, dim3(heads * q_slices), dim3(kTopkThreads), 0, stream, probs, nq, nk,
+                     q_slices, topk, mask_out, sel, kidx, kcnt);
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+}  // namespace fvsr

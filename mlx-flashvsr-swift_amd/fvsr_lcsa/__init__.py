@@ -1,0 +1,322 @@
+"""Python host binding of libfvsr_lcsa (the MI355X LCSA path) over torch device tensors.
+
+Names mirror the reference's call surface (xocialize/mlx-flashvsr-swift):
+  local_block_mask            localBlockMask(bh:bw:range:)                    DiT.swift:130-145
+  draft_block_mask_and_probs  draftBlockMaskAndProbs(qW:kW:heads:qSlices:...)  DiT.swift:158-174
+  draft_block_mask            draftBlockMask(...)                              DiT.swift:150-154
+  kernel_block_attention      kernelBlockAttention(q:k:v:blockMask:heads:)     SparseAttention.swift:169-187
+  block_masked_attention      blockMaskedAttention(q:k:v:blockMask:heads:)     DiT.swift:279-313 (dense fallback)
+  FlashVSRAttentionOps        FlashVSRAttentionOps.dense / .kernel             SparseAttention.swift:190-202
+  KVRing                      the window K/V cache of blockForward             DiT.swift:507-511,532-538
+  window_partition / reverse  windowPartition / windowReverse                  DiT.swift:113-126
+Token tensors are (L, H*128) or (1, L, H*128), window order, float32 or bfloat16, on a HIP device, contiguous.
+Every call runs the HIP kernels of libfvsr_lcsa.so; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _abi
+from ._abi import (ATTN_AUTO, ATTN_DENSE, ATTN_KERNEL, DTYPE_BF16, DTYPE_F32, LAYOUT_GRID, LAYOUT_WINDOWS,
+                   FVSRError, call, lib)
+
+__all__ = ["FVSRError", "Context", "local_block_mask", "draft_block_mask_and_probs", "draft_block_mask",
+           "kernel_block_attention", "block_masked_attention", "block_sparse_attention", "FlashVSRAttentionOps",
+           "KVRing", "window_partition", "window_reverse", "attention_mode_auto", "workspace_size",
+           "ATTN_AUTO", "ATTN_DENSE", "ATTN_KERNEL", "LAYOUT_GRID", "LAYOUT_WINDOWS", "lib"]
+
+HEAD_DIM = 128
+BLOCK = 128
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise FVSRError(_abi.ERR_INVALID_ARG, "dtype", f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+
+
+def _tokens(x: torch.Tensor, name: str) -> torch.Tensor:
+    if x.dim() == 3:
+        if x.shape[0] != 1:
+            raise FVSRError(_abi.ERR_UNSUPPORTED, name, "batch 1 only (the reference asserts the same)")
+        x = x[0]
+    if x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, "expected a contiguous (L, C) device tensor")
+    return x
+
+
+def _ptr(t) -> C.c_void_p:
+    return C.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _stream(stream) -> C.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+class Context:
+    """One fvsr_ctx per device (workspace + device binding). Not re-entrant, like the reference's modules."""
+    _by_device: dict[int, "Context"] = {}
+
+    def __init__(self, device: int = 0):
+        self.device = device
+        h = C.c_void_p()
+        call("fvsr_ctx_create", device, C.byref(h))
+        self.handle = h
+        self._local_cache: dict[tuple, torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device: int | torch.device | None = None) -> "Context":
+        if device is None:
+            device = torch.cuda.current_device()
+        if isinstance(device, torch.device):
+            device = device.index if device.index is not None else torch.cuda.current_device()
+        if device not in cls._by_device:
+            cls._by_device[device] = Context(device)
+        return cls._by_device[device]
+
+    def reserve(self, nbytes: int):
+        call("fvsr_ctx_reserve", self.handle, nbytes)
+
+    def workspace_bytes(self) -> int:
+        return int(lib.fvsr_ctx_workspace_bytes(self.handle))
+
+    def local_device(self, local) -> torch.Tensor:
+        """Device copy of an (s, s) local window mask, memoised by content (the reference memoises per geometry,
+        DiT.swift:464-470)."""
+        if isinstance(local, torch.Tensor) and local.is_cuda:
+            return local.to(torch.uint8).contiguous()
+        arr = np.ascontiguousarray(np.asarray(local, dtype=np.uint8))
+        key = (arr.shape, arr.tobytes())
+        t = self._local_cache.get(key)
+        if t is None:
+            t = torch.from_numpy(arr.copy()).to(f"cuda:{self.device}")
+            self._local_cache[key] = t
+        return t
+
+    def __del__(self):
+        try:
+            lib.fvsr_ctx_destroy(self.handle)
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# host helpers
+# ------------------------------------------------------------------------------------------------------------------
+def local_block_mask(bh: int, bw: int, r: int) -> np.ndarray:
+    """(s, s) bool local window (host). localBlockMask, DiT.swift:130-145."""
+    s = bh * bw
+    out = np.zeros((s, s), dtype=np.uint8)
+    call("fvsr_local_block_mask", bh, bw, r, out.ctypes.data_as(C.c_void_p))
+    return out.astype(bool)
+
+
+def attention_mode_auto(topk: int, s: int, nk: int, threshold: float = 0.45):
+    """(expected kept fraction, ATTN_KERNEL | ATTN_DENSE): the `auto` rule of DiT.swift:517-522."""
+    e = C.c_double()
+    m = C.c_int()
+    call("fvsr_attention_mode_auto", topk, s, nk, threshold, C.byref(e), C.byref(m))
+    return e.value, m.value
+
+
+def workspace_size(heads: int, lq: int, lk: int, channels: int) -> int:
+    return int(lib.fvsr_workspace_size(heads, lq, lk, channels))
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# selection
+# ------------------------------------------------------------------------------------------------------------------
+def draft_block_mask_and_probs(qW: torch.Tensor, kW: torch.Tensor, heads: int, q_slices: int, s: int, local,
+                               topk: int, stream=None, want_mask: bool = True, want_probs: bool = True):
+    """Returns (mask (H, Nq, Nk) f32 0/1 or None, probs (H, Nq, Nk) f32 or None, kidx (H, Nq, Nk) i32,
+    kcnt (H, Nq) i32). DiT.swift:158-174 + SparseAttention.swift:175-177."""
+    q = _tokens(qW.reshape(-1, qW.shape[-1]) if qW.dim() == 3 and qW.shape[0] != 1 else qW, "qW")
+    k = _tokens(kW.reshape(-1, kW.shape[-1]) if kW.dim() == 3 and kW.shape[0] != 1 else kW, "kW")
+    ctx = Context.get(q.device)
+    nq = -(-q.shape[0] // BLOCK)
+    nk = -(-k.shape[0] // BLOCK)
+    dev = q.device
+    mask = torch.empty((heads, nq, nk), dtype=torch.float32, device=dev) if want_mask else None
+    probs = torch.empty((heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
+    kidx = torch.empty((heads, nq, nk), dtype=torch.int32, device=dev)
+    kcnt = torch.empty((heads, nq), dtype=torch.int32, device=dev)
+    loc = ctx.local_device(local)
+    call("fvsr_lcsa_select", ctx.handle, _dtype_code(q), _ptr(q), q.shape[0], _ptr(k), k.shape[0], heads, q_slices,
+         s, _ptr(loc), topk, _ptr(mask), _ptr(probs), _ptr(kidx), _ptr(kcnt), _stream(stream))
+    return mask, probs, kidx, kcnt
+
+
+def draft_block_mask(qW, kW, heads, q_slices, s, local, topk, stream=None) -> torch.Tensor:
+    return draft_block_mask_and_probs(qW, kW, heads, q_slices, s, local, topk, stream, want_probs=False)[0]
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# attention
+# ------------------------------------------------------------------------------------------------------------------
+def _attn_mask(q, k, v, block_mask, heads, mode, stream, out):
+    shape = q.shape
+    q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+    if not (q2.dtype == k2.dtype == v2.dtype):
+        raise FVSRError(_abi.ERR_INVALID_ARG, "attention", "q, k, v dtypes differ")
+    bm = block_mask.to(torch.float32).contiguous()
+    ctx = Context.get(q2.device)
+    o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+    call("fvsr_lcsa_attention_mask", ctx.handle, _dtype_code(q2), _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2),
+         k2.shape[0], heads, _ptr(bm), mode, _ptr(o), _stream(stream))
+    return o.reshape(shape)
+
+
+def kernel_block_attention(q, k, v, block_mask, heads: int, stream=None, out=None) -> torch.Tensor:
+    """Block-sparse kernel: visits only the selected key blocks. SparseAttention.swift:169-187."""
+    return _attn_mask(q, k, v, block_mask, heads, ATTN_KERNEL, stream, out)
+
+
+def block_masked_attention(q, k, v, block_mask, heads: int, stream=None, out=None) -> torch.Tensor:
+    """Dense fallback: the same kernel walks every key block, unselected ones masked. DiT.swift:279-313."""
+    return _attn_mask(q, k, v, block_mask, heads, ATTN_DENSE, stream, out)
+
+
+def block_sparse_attention(q, k, v, kidx, kcnt, heads: int, stream=None, out=None) -> torch.Tensor:
+    """Attention from (kidx, kcnt) lists: the Metal launch ABI of SparseAttention.swift:180-185."""
+    shape = q.shape
+    q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+    ctx = Context.get(q2.device)
+    kidx = kidx.to(torch.int32).contiguous()
+    kcnt = kcnt.to(torch.int32).contiguous()
+    o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+    call("fvsr_lcsa_attention", ctx.handle, _dtype_code(q2), _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2), k2.shape[0],
+         heads, _ptr(kidx), _ptr(kcnt), kidx.shape[-1], _ptr(o), _stream(stream))
+    return o.reshape(shape)
+
+
+class FlashVSRAttentionOps:
+    """Public probe entry points (SparseAttention.swift:190-202). `gathered` is not built (study-only upstream)."""
+
+    @staticmethod
+    def dense(q, k, v, block_mask, heads: int, stream=None):
+        return block_masked_attention(q, k, v, block_mask, heads, stream)
+
+    @staticmethod
+    def kernel(q, k, v, block_mask, heads: int, stream=None):
+        return kernel_block_attention(q, k, v, block_mask, heads, stream)
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# layout
+# ------------------------------------------------------------------------------------------------------------------
+def _layout(x, f, h, w, to_windows, stream):
+    shape = x.shape
+    x2 = _tokens(x, "x")
+    out = torch.empty_like(x2)
+    name = "fvsr_window_partition" if to_windows else "fvsr_window_reverse"
+    call(name, _dtype_code(x2), _ptr(x2), _ptr(out), f, h, w, x2.shape[1], _stream(stream))
+    return out.reshape(shape)
+
+
+def window_partition(x, f: int, h: int, w: int, stream=None):
+    """(F*H*W, C) natural order -> window order (as a flat (L, C) token tensor). DiT.swift:113-118."""
+    return _layout(x, f, h, w, True, stream)
+
+
+def window_reverse(x, f: int, h: int, w: int, stream=None):
+    """Window order -> natural (F*H*W, C) order. DiT.swift:121-126."""
+    return _layout(x, f, h, w, False, stream)
+
+
+# ------------------------------------------------------------------------------------------------------------------
+# KV ring
+# ------------------------------------------------------------------------------------------------------------------
+class KVRing:
+    """Streaming window K/V cache for `layers` DiT blocks (DiT.swift:507-511,532-538; Pipeline.swift:87-91)."""
+
+    def __init__(self, layers: int, heads: int, bh: int, bw: int, capacity: int = 4, kv_len: int = 3,
+                 dtype: torch.dtype = torch.bfloat16, device: int | None = None):
+        self.ctx = Context.get(device)
+        self.layers, self.heads, self.bh, self.bw = layers, heads, bh, bw
+        self.s = bh * bw
+        self.capacity, self.kv_len = capacity, kv_len
+        self.dtype = dtype
+        self.code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F32
+        h = C.c_void_p()
+        call("fvsr_kv_ring_create", self.ctx.handle, self.code, layers, heads, bh, bw, capacity, kv_len, C.byref(h))
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            lib.fvsr_kv_ring_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        call("fvsr_kv_ring_reset", self.handle)
+
+    def append(self, layer: int, k_new, v_new, n_slices: int, layout: int = LAYOUT_WINDOWS, stream=None):
+        k2, v2 = _tokens(k_new, "k_new"), _tokens(v_new, "v_new")
+        call("fvsr_kv_ring_append", self.handle, layer, _ptr(k2), _ptr(v2), n_slices, layout, _stream(stream))
+
+    def evict(self, layer: int):
+        call("fvsr_kv_ring_evict", self.handle, layer)
+
+    def slices(self, layer: int) -> int:
+        n = C.c_int()
+        call("fvsr_kv_ring_slices", self.handle, layer, C.byref(n))
+        return n.value
+
+    def read(self, layer: int, stream=None):
+        n = self.slices(layer) * self.s * BLOCK
+        ch = self.heads * HEAD_DIM
+        dev = f"cuda:{self.ctx.device}"
+        k = torch.empty((n, ch), dtype=self.dtype, device=dev)
+        v = torch.empty((n, ch), dtype=self.dtype, device=dev)
+        call("fvsr_kv_ring_read", self.handle, layer, _ptr(k), _ptr(v), _stream(stream))
+        return k, v
+
+    def select(self, layer: int, qW, q_slices: int, local, topk: int, stream=None, want_mask=True, want_probs=True):
+        q = _tokens(qW, "qW")
+        nq = -(-q.shape[0] // BLOCK)
+        nk = self.slices(layer) * self.s
+        dev = q.device
+        mask = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_mask else None
+        probs = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
+        kidx = torch.empty((self.heads, nq, nk), dtype=torch.int32, device=dev)
+        kcnt = torch.empty((self.heads, nq), dtype=torch.int32, device=dev)
+        call("fvsr_lcsa_select_ring", self.ctx.handle, self.handle, layer, _ptr(q), q.shape[0], q_slices,
+             _ptr(self.ctx.local_device(local)), topk, _ptr(mask), _ptr(probs), _ptr(kidx), _ptr(kcnt),
+             _stream(stream))
+        return mask, probs, kidx, kcnt
+
+    def attention(self, layer: int, q, kidx, kcnt, mode: int = ATTN_KERNEL, stream=None, out=None):
+        q2 = _tokens(q, "q")
+        o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+        call("fvsr_lcsa_attention_ring", self.ctx.handle, self.handle, layer, _ptr(q2), q2.shape[0], _ptr(kidx),
+             _ptr(kcnt), kidx.shape[-1], mode, _ptr(o), _stream(stream))
+        return o
+
+    def layer_call(self, layer: int, qW, k_new, v_new, n_new_slices: int, q_slices: int, local, topk: int,
+                   mode: int = ATTN_AUTO, layout: int = LAYOUT_WINDOWS, stream=None, out=None, want_mask=False,
+                   want_probs=False):
+        """append -> select -> attention -> evict: the LCSA core of blockForward (DiT.swift:504-538)."""
+        q2 = _tokens(qW, "qW")
+        k2, v2 = _tokens(k_new, "k_new"), _tokens(v_new, "v_new")
+        o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+        nq = -(-q2.shape[0] // BLOCK)
+        nk = (self.slices(layer) + n_new_slices) * self.s
+        dev = q2.device
+        mask = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_mask else None
+        probs = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
+        call("fvsr_lcsa_layer", self.ctx.handle, self.handle, layer, _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2),
+             n_new_slices, layout, q_slices, _ptr(self.ctx.local_device(local)), topk, mode, _ptr(o), _ptr(mask),
+             _ptr(probs), _stream(stream))
+        return o, mask, probs

@@ -1,0 +1,187 @@
+"""GPU parity of the block-sparse attention (lcsa_attn) through the C ABI, against the oracle.
+
+Bars (written in each test): fp32 rel <= 1e-5, bf16 rel <= 1e-2 against the float64 oracle on the same (bf16-valued)
+inputs, rel = max|got - ref| / max|ref| (Gates.swift:19-29). The kernel and its dense fallback must agree exactly.
+The reference's own probe protocol (Diag.swift:86-121: random masks at 0.3-0.6 density with a forced empty query
+block, fp32 and bf16) is reproduced.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import fvsr_lcsa
+from fvsr_lcsa import synth
+from oracle import lcsa as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "lcsa_tiny.npz")
+FP32_REL = 1e-5
+BF16_REL = 1e-2
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _rel(got, ref):
+    return O.compare(_np(got) if isinstance(got, torch.Tensor) else got, ref)["rel"]
+
+
+def test_golden_fixture_fp32(dev):
+    g = np.load(GOLDEN)
+    heads = int(g["meta"][0])
+    q, k, v = (torch.from_numpy(g[n]).to(dev) for n in ("q", "k", "v"))
+    mask = torch.from_numpy(g["mask"]).to(dev)
+    o = fvsr_lcsa.kernel_block_attention(q, k, v, mask, heads)
+    od = fvsr_lcsa.block_masked_attention(q, k, v, mask, heads)
+    assert _rel(o, g["out"]) <= FP32_REL
+    assert torch.equal(o, od)
+
+
+def test_golden_fixture_bf16(dev):
+    g = np.load(GOLDEN)
+    heads = int(g["meta"][0])
+    # fixture inputs are multiples of 1/16 in [-4, 4]: exact in bf16
+    q, k, v = (torch.from_numpy(g[n]).to(dev).to(torch.bfloat16) for n in ("q", "k", "v"))
+    assert torch.equal(q.float().cpu(), torch.from_numpy(g["q"]))
+    mask = torch.from_numpy(g["mask"]).to(dev)
+    o = fvsr_lcsa.kernel_block_attention(q, k, v, mask, heads)
+    assert o.dtype == torch.bfloat16
+    assert _rel(o, g["out"]) <= BF16_REL
+
+
+@pytest.mark.parametrize("dtype,lqb,lkb,density", [(torch.float32, 4, 6, 0.5), (torch.float32, 12, 36, 0.3),
+                                                   (torch.bfloat16, 12, 36, 0.6)])
+def test_reference_probe_protocol(dev, dtype, lqb, lkb, density):
+    """Diag.swift:87-97: 2 heads, random q/k/v, uniform random block mask, one forced empty query block."""
+    heads = 2
+    gen = torch.Generator().manual_seed(lqb * 100 + lkb)
+    q = torch.randn((lqb * 128, heads * 128), generator=gen).to(dtype)
+    k = torch.randn((lkb * 128, heads * 128), generator=gen).to(dtype)
+    v = torch.randn((lkb * 128, heads * 128), generator=gen).to(dtype)
+    m = (torch.rand((heads, lqb, lkb), generator=gen) < density).float()
+    m[0, 1] = 0
+    ref = O.block_masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), m.numpy(), heads)
+    o = fvsr_lcsa.FlashVSRAttentionOps.kernel(q.to(dev), k.to(dev), v.to(dev), m.to(dev), heads)
+    od = fvsr_lcsa.FlashVSRAttentionOps.dense(q.to(dev), k.to(dev), v.to(dev), m.to(dev), heads)
+    bar = FP32_REL if dtype == torch.float32 else BF16_REL
+    assert _rel(o, ref) <= bar
+    assert torch.equal(o, od)
+    assert (o[128:256, :128] == 0).all()          # the forced empty query block
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("lq,lk", [(200, 300), (128, 129), (77, 1000), (384, 64)])
+def test_ragged_tails(dev, dtype, lq, lk):
+    heads = 2
+    gen = torch.Generator().manual_seed(lq + lk)
+    q = torch.randn((lq, heads * 128), generator=gen).to(dtype)
+    k = torch.randn((lk, heads * 128), generator=gen).to(dtype)
+    v = torch.randn((lk, heads * 128), generator=gen).to(dtype)
+    nq, nk = -(-lq // 128), -(-lk // 128)
+    m = (torch.rand((heads, nq, nk), generator=gen) < 0.7).float()
+    m[:, :, -1] = 1                                # always touch the ragged key block
+    ref = O.block_masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), m.numpy(), heads)
+    o = fvsr_lcsa.kernel_block_attention(q.to(dev), k.to(dev), v.to(dev), m.to(dev), heads)
+    assert o.shape == (lq, heads * 128)
+    assert _rel(o, ref) <= (FP32_REL if dtype == torch.float32 else BF16_REL)
+
+
+def test_all_empty_mask_gives_zeros(dev):
+    heads = 3
+    q = torch.randn((256, heads * 128), device=dev)
+    k = torch.randn((512, heads * 128), device=dev)
+    m = torch.zeros((heads, 2, 4), device=dev)
+    o = torch.full_like(q, 7.0)
+    fvsr_lcsa.kernel_block_attention(q, k, k, m, heads, out=o)
+    assert (o == 0).all()
+    o.fill_(7.0)
+    fvsr_lcsa.block_masked_attention(q, k, k, m, heads, out=o)
+    assert (o == 0).all()
+
+
+def test_list_order_does_not_change_the_result(dev):
+    heads = 2
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn((512, heads * 128), generator=gen)
+    k = torch.randn((1024, heads * 128), generator=gen)
+    v = torch.randn((1024, heads * 128), generator=gen)
+    m = (torch.rand((heads, 4, 8), generator=gen) < 0.5).float()
+    kidx, kcnt = O.block_lists(m.numpy())
+    rev = kidx.copy()
+    for h in range(heads):
+        for i in range(4):
+            c = kcnt[h, i]
+            rev[h, i, :c] = kidx[h, i, :c][::-1]
+    a = fvsr_lcsa.block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(kidx).to(dev),
+                                         torch.from_numpy(kcnt).to(dev), heads)
+    b = fvsr_lcsa.block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(rev).to(dev),
+                                         torch.from_numpy(kcnt).to(dev), heads)
+    assert O.compare(_np(a), _np(b))["rel"] <= 1e-6
+
+
+def test_c1_fp32_parity(dev):
+    """512x512 fp32 workload: Lq 2048, Lk 6144, 12 heads, the oracle's own mask; rel <= 1e-5."""
+    wl = synth.WORKLOADS["lcsa_512x512_fp32"]
+    q, k, v = synth.make_qkv(wl, seed=0)
+    local = synth.local_mask(wl).numpy()
+    topk = synth.workload_topk(wl)
+    mask, _ = O.draft_block_mask_and_probs(q.numpy(), k.numpy(), wl.heads, wl.q_slices, wl.s, local, topk)
+    ref = O.block_masked_attention(q.numpy(), k.numpy(), v.numpy(), mask, wl.heads)
+    md = torch.from_numpy(mask).to(dev)
+    o = fvsr_lcsa.kernel_block_attention(q.to(dev), k.to(dev), v.to(dev), md, wl.heads)
+    od = fvsr_lcsa.block_masked_attention(q.to(dev), k.to(dev), v.to(dev), md, wl.heads)
+    assert _rel(o, ref) <= FP32_REL
+    assert torch.equal(o, od)
+
+
+def _torch_fp32_attention(q, k, v, heads, hsel):
+    """Plain torch fp32 attention for the heads in `hsel` (full mask), one head at a time on the device."""
+    d = 128
+    outs = []
+    for h in hsel:
+        qh = q[:, h * d:(h + 1) * d].float()
+        kh = k[:, h * d:(h + 1) * d].float()
+        vh = v[:, h * d:(h + 1) * d].float()
+        s = (qh @ kh.t().contiguous()) / d ** 0.5
+        outs.append(torch.softmax(s, dim=-1) @ vh)
+    return torch.cat(outs, dim=1)
+
+
+def test_c2_full_mask_sparse_equals_dense_bf16(dev):
+    """1280x768 bf16, every block kept: kernel == dense fallback exactly, and both within 1e-2 of torch fp32."""
+    wl = synth.WORKLOADS["dense_1280x768_bf16"]
+    q, k, v = synth.make_qkv(wl, seed=0, device=dev)
+    m = torch.ones((wl.heads, wl.nq, wl.nk), device=dev)
+    o = fvsr_lcsa.kernel_block_attention(q, k, v, m, wl.heads)
+    od = fvsr_lcsa.block_masked_attention(q, k, v, m, wl.heads)
+    assert torch.equal(o, od)
+    hsel = [0, 7]
+    ref = _torch_fp32_attention(q, k, v, wl.heads, hsel)
+    got = torch.cat([o[:, h * 128:(h + 1) * 128] for h in hsel], dim=1)
+    rel = ((got.float() - ref).abs().max() / ref.abs().max()).item()
+    assert rel <= BF16_REL
+
+
+def test_c4_bf16_subset_vs_oracle(dev):
+    """1920x1152 bf16 (Lq 17280, Lk 43200 with a ragged last key block), mask from the GPU selection; a subset of
+    (head, query block) rows against the float64 oracle at rel <= 1e-2, and kernel == dense fallback everywhere."""
+    wl = synth.WORKLOADS["sparse_1920x1152_bf16"]
+    q, k, v = synth.make_qkv(wl, seed=0)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    local = synth.local_mask(wl).numpy()
+    mask, _, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(qd, kd, wl.heads, wl.q_slices, wl.s, local,
+                                                               synth.workload_topk(wl), want_probs=False)
+    o = fvsr_lcsa.kernel_block_attention(qd, kd, vd, mask, wl.heads)
+    od = fvsr_lcsa.block_masked_attention(qd, kd, vd, mask, wl.heads)
+    assert torch.equal(o, od)
+    heads_sel, qb_sel = [0, 5, 11], [0, 67, 134]
+    ref = O.block_masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask.cpu().numpy(),
+                                   wl.heads, heads_subset=heads_sel, qblocks_subset=qb_sel)
+    got = _np(o)
+    rows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in qb_sel])
+    cols = np.concatenate([np.arange(h * 128, h * 128 + 128) for h in heads_sel])
+    assert O.compare(got[np.ix_(rows, cols)], ref[np.ix_(rows, cols)])["rel"] <= BF16_REL
+    assert torch.isfinite(o.float()).all()
