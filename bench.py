@@ -1,0 +1,232 @@
+"""Benchmark of the LCSA layer call on one MI355X.
+
+A step is one LCSA layer call of the DiT self-attention block on the 1920x1152 workload (bf16, 12 heads x 128,
+Lq 17280 = 2 latent frames, Lk 43200 = 5 latent frames incl. cache, local range 11, 30% of the in-window block pairs
+kept, per-head RMS-normed Q/K with 3-D RoPE): block selection (pool Q and K, block scores, softmax, exact per-(head,
+slice) top-k, key lists) followed by the block-sparse attention over the kept 128x128 blocks. Inputs are resident in
+HBM before the timed region. Throughput counts kept-block FLOPs only (4 * 128 * valid q tokens * valid k tokens per
+kept (head, q-block, k-block)).
+
+Printed: one JSON line (rank 0) with the layer-call rate, the attention kernel's MFMA roofline fraction (kernel time
+from HIP events on the launch stream), the same kernel's dense fallback time, and the CPU oracle timed on a bounded
+sample on the host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "mlx-flashvsr-swift_amd")
+for p in (PKG, ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "block-sparse attn ms/layer-call + effective TFLOP/s (% MFMA peak), 1920×1152"
+PEAK_BF16_TFLOPS = 2500.0            # MI355X dense bf16 MFMA
+PROFILE_PMC = os.path.join(ROOT, "profiles", "lcsa_attn_bf16_1920x1152_pmc.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="sparse_1920x1152_bf16")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--attn-only", action="store_true", help="time only the attention kernel loop (profiling)")
+    return ap.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary (null if absent)."""
+    try:
+        with open(PROFILE_PMC) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
+    """The oracle on the host: selection over the whole workload plus attention over a sample of (head, query
+    block) rows, scaled to one layer call."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from fvsr_lcsa import synth
+    from oracle import lcsa as O
+
+    qn, kn, vn = (t.float().cpu().numpy() for t in (q, k, v))
+    local = synth.local_mask(wl).numpy()
+    topk = synth.workload_topk(wl)
+    t0 = time.perf_counter()
+    O.draft_block_mask_and_probs(qn, kn, wl.heads, wl.q_slices, wl.s, local, topk, lk=wl.lk)
+    t_sel = time.perf_counter() - t0
+    m = mask.cpu().numpy()
+    rows = [(h, i) for h in range(wl.heads) for i in range(wl.nq)]
+    rng = np.random.default_rng(0)
+    order = rng.permutation(len(rows))
+    done, t_att = [], 0.0
+    for idx in order:
+        h, i = rows[idx]
+        t0 = time.perf_counter()
+        O.block_masked_attention(qn, kn, vn, m, wl.heads, dtype=np.float32, heads_subset=[h], qblocks_subset=[i])
+        t_att += time.perf_counter() - t0
+        done.append((h, i))
+        if t_att + t_sel >= budget_s and len(done) >= 4:
+            break
+    # kept FLOPs of the sampled rows vs all rows
+    def row_flops(h, i):
+        sel = np.nonzero(m[h, i] > 0.5)[0]
+        keys = sum(min(128, wl.lk - j * 128) for j in sel)
+        return 4.0 * 128 * min(128, wl.lq - i * 128) * keys
+    sample_flops = sum(row_flops(h, i) for h, i in done)
+    t_layer = t_sel + t_att * kept_flops_total / max(sample_flops, 1.0)
+    threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    return {
+        "value": kept_flops_total / t_layer / 1e12,
+        "unit": "TFLOP/s (effective, kept blocks)",
+        "ms_per_layer_call": t_layer * 1e3,
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"oracle (numpy fp32) selection over the full workload ({t_sel:.2f} s) + block-masked attention "
+                  f"over {len(done)} of {len(rows)} (head, query block) rows ({t_att:.2f} s), scaled by kept FLOPs",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import fvsr_lcsa
+    from fvsr_lcsa import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    wl = synth.WORKLOADS[args.workload]
+    q, k, v = synth.make_qkv(wl, seed=args.seed, device=dev)
+    local = synth.local_mask(wl).numpy()
+    topk = synth.workload_topk(wl)
+    ctx = fvsr_lcsa.Context.get(dev)
+    ctx.reserve(fvsr_lcsa.workspace_size(wl.heads, wl.lq, wl.lk, wl.channels))
+    stream = torch.cuda.current_stream()
+    o = torch.empty_like(q)
+
+    def select():
+        return fvsr_lcsa.draft_block_mask_and_probs(q, k, wl.heads, wl.q_slices, wl.s, local, topk,
+                                                    want_mask=False, want_probs=False)
+
+    def attend(kidx, kcnt):
+        fvsr_lcsa.block_sparse_attention(q, k, v, kidx, kcnt, wl.heads, out=o)
+
+    # reference selection for FLOP counting and the dense fallback
+    mask, _, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q, k, wl.heads, wl.q_slices, wl.s, local, topk,
+                                                               want_probs=False)
+    torch.cuda.synchronize()
+    kept = synth.kept_flops(kcnt, kidx, wl.lq, wl.lk)
+    kept_fraction = float(kcnt.sum().item()) / (wl.heads * wl.nq * wl.nk)
+
+    for _ in range(args.warmup):
+        _, _, ki, kc = select()
+        attend(ki, kc)
+    torch.cuda.synchronize()
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for i in range(args.steps):
+        if args.attn_only:
+            a0, a1 = ev[i]
+            a0.record(stream)
+            attend(kidx, kcnt)
+            a1.record(stream)
+            continue
+        _, _, ki, kc = select()
+        a0, a1 = ev[i]
+        a0.record(stream)
+        attend(ki, kc)
+        a1.record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = t_start.elapsed_time(t_end) / args.steps
+    ms_attn = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    ms_select = ms_step - ms_attn
+
+    # dense fallback: the same kernel walking every key block (masked), same inputs
+    od = torch.empty_like(q)
+    for _ in range(2):
+        fvsr_lcsa.block_masked_attention(q, k, v, mask, wl.heads, out=od)
+    torch.cuda.synchronize()
+    nd = max(3, args.steps // 4)
+    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    d0.record(stream)
+    for _ in range(nd):
+        fvsr_lcsa.block_masked_attention(q, k, v, mask, wl.heads, out=od)
+    d1.record(stream)
+    torch.cuda.synchronize()
+    ms_dense = d0.elapsed_time(d1) / nd    # includes the mask -> list build (a few us)
+
+    achieved = kept / (ms_attn * 1e-3) / 1e12
+    value = kept / (ms_step * 1e-3) / 1e12
+    traffic = read_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s (effective, kept blocks; whole layer call = selection + attention)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1), per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)",
+        "config": {
+            "workload": wl.name,
+            "description": wl.description,
+            "heads": wl.heads, "head_dim": 128, "lq": wl.lq, "lk": wl.lk, "q_blocks": wl.nq, "k_blocks": wl.nk,
+            "spatial_blocks_per_slice": wl.s, "local_range": wl.local_range, "topk": topk,
+            "kept_block_fraction": round(kept_fraction, 4), "kept_tflop": round(kept / 1e12, 4),
+        },
+        "breakdown_ms": {
+            "layer_call": round(ms_step, 4),
+            "attention_kernel": round(ms_attn, 4),
+            "selection": round(ms_select, 4),
+            "dense_fallback_attention": round(ms_dense, 4),
+        },
+        "attention_tflops": round(achieved, 2),
+        "sparse_vs_dense_speedup": round(ms_dense / ms_attn, 3),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+        },
+        "host_wall_s": round(wall, 3),
+    }
+    if not args.no_cpu and not args.attn_only:
+        line["cpu_baseline"] = cpu_baseline(wl, q, k, v, mask, kept, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -255,6 +255,7 @@ static AttnArgs make_args(const void* q, int64_t lq, const void* k, const void* 
   a.nq = (int)ceil_div(lq, kBlock);
   a.nk = nk;
   a.map = map;
+  a.kv_rows = lk;
   a.c = (float)(1.4426950408889634 / std::sqrt((double)kHeadDim));
   return a;
 }
@@ -268,6 +269,9 @@ static int check_attn_common(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq
   FVSR_REQUIRE(q && k && v && o, FVSR_ERR_INVALID_ARG, "q, k, v and o must be non-NULL");
   FVSR_REQUIRE(lq > 0 && lk > 0, FVSR_ERR_INVALID_ARG, "lq and lk must be > 0");
   FVSR_REQUIRE((int64_t)heads * ceil_div(lq, kBlock) < (int64_t)1 << 31, FVSR_ERR_UNSUPPORTED, "grid too large");
+  // K/V are addressed with 32-bit buffer offsets
+  FVSR_REQUIRE(lk * heads * kHeadDim * esize(dtype) < ((int64_t)1 << 31), FVSR_ERR_UNSUPPORTED,
+               "k/v buffers above 2 GiB are not supported");
   return FVSR_OK;
 }
 
@@ -350,6 +354,10 @@ int fvsr_kv_ring_create(fvsr_ctx* ctx, int dtype, int layers, int heads, int bh,
   r->head.assign(layers, 0);
   r->count.assign(layers, 0);
   const size_t kv_bytes = (size_t)layers * r->layer_tokens() * r->C * esize(dtype);
+  if ((int64_t)r->layer_tokens() * r->C * esize(dtype) >= ((int64_t)1 << 31)) {
+    delete r;
+    return set_error(FVSR_ERR_UNSUPPORTED, "a ring layer above 2 GiB is not supported (32-bit buffer offsets)");
+  }
   const size_t pooled_bytes = (size_t)layers * capacity_slices * r->s * r->C * sizeof(float);
   if (hipSetDevice(ctx->device) != hipSuccess || hipMalloc(&r->k, kv_bytes) != hipSuccess ||
       hipMalloc(&r->v, kv_bytes) != hipSuccess || hipMalloc((void**)&r->pooled, pooled_bytes) != hipSuccess) {
@@ -454,8 +462,9 @@ static int attention_ring_impl(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const 
                                const int32_t* kidx, const int32_t* kcnt, int nk_stride, const uint8_t* sel,
                                bool dense, void* o, hipStream_t stream) {
   const int nk = r->count[layer] * r->s;
-  const AttnArgs a = make_args(q, lq, r->layer_k(layer), r->layer_v(layer), (int64_t)nk * kBlock, r->heads, kidx,
-                               kcnt, sel, nk_stride, nk, r->map(layer), o);
+  AttnArgs a = make_args(q, lq, r->layer_k(layer), r->layer_v(layer), (int64_t)nk * kBlock, r->heads, kidx, kcnt,
+                         sel, nk_stride, nk, r->map(layer), o);
+  a.kv_rows = (int64_t)r->layer_tokens();
   return launch_attention(r->dtype, dense, a, stream);
 }
 

@@ -11,6 +11,7 @@ namespace fvsr {
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -70,6 +71,7 @@ struct AttnArgs {
   int nq;
   int nk;
   KeyMap map;
+  int64_t kv_rows;       // token rows physically present in the k/v buffers (buffer-load range)
   float c;               // softmax scale * log2(e)
 };
 
