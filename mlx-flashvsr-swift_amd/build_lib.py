@@ -52,7 +52,7 @@ def build(verbose: bool = False) -> str:
     probe_src = os.path.join(HOST, "probe_attn.cpp")
     if os.path.exists(probe_src):
         ptmp = PROBE + ".tmp"
-        _run([hipcc, "-O2", "-std=c++17", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", probe_src,
+        _run([hipcc, *HIP_FLAGS, "-x", "hip", f"-I{os.path.join(ROOT, 'include')}", f"-I{HOST}", probe_src,
               f"-L{LIB_DIR}", "-lfvsr_lcsa", f"-Wl,-rpath,$ORIGIN", "-o", ptmp], verbose)
         os.replace(ptmp, PROBE)
     return LIB
