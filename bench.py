@@ -40,6 +40,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="time only the attention kernel loop (profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain copy of known size (the window-partition kernel over 16x72x120 bf16 "
+                         "tokens of 1536 channels: 424.7 MB read + 424.7 MB written per launch), the reference "
+                         "point that scales the FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -102,6 +106,29 @@ def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
     }
 
 
+def copy_calibration(steps: int):
+    """A plain copy of known size: window_partition reads and writes every byte exactly once."""
+    import torch
+
+    import fvsr_lcsa
+
+    f, h, w, ch = 16, 72, 120, 1536
+    x = torch.randn((f * h * w, ch), device="cuda:0").to(torch.bfloat16)
+    nbytes = x.numel() * 2
+    for _ in range(2):
+        fvsr_lcsa.window_partition(x, f, h, w)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fvsr_lcsa.window_partition(x, f, h, w)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "ms": round(ms, 4),
+                                           "GB/s": round(2 * nbytes / ms / 1e6, 1)}}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -114,6 +141,9 @@ def main():
     from fvsr_lcsa import synth
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
     dev = torch.device("cuda:0")
     wl = synth.WORKLOADS[args.workload]
     q, k, v = synth.make_qkv(wl, seed=args.seed, device=dev)
