@@ -4,16 +4,14 @@
 // blockMaskedAttention (DiT.swift:279-313): per head, o = softmax(q k^T / sqrt(128)) v over the listed key blocks,
 // fp32 online softmax, a query block with no listed key block writes zeros.
 //
-// Design (not the reference's): one workgroup = one (head, 128-query block); 4 wave64s x 32 queries.
-//   S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (keys = M, queries = N), so each lane owns ONE query row: the row max and
-//   row sum are per-lane scalars (plus one permlane32 swap), no LDS round trip.
-//   O^T += V^T P^T on the same MFMA: P^T comes straight from the S^T accumulator registers (bf16-packed), V^T is read
-//   from row-major LDS with ds_read_b64_tr_b16, so V needs no transpose anywhere.
-//   K/V tiles of 64 keys are double-buffered in LDS (70 KB per workgroup -> 2 workgroups per CU), prefetched to
-//   registers one tile ahead; padded LDS rows keep the MFMA operand reads bank-conflict free.
-//   Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of (head, query block) items: adjacent
-//   query blocks select overlapping key blocks (spatial locality), so K/V tiles hit in L2.
-// fp32 I/O (the parity lane) runs the same scheme on v_mfma_f32_32x32x2_f32 with 32-key fp32 tiles.
+// bf16 (the production lane): one workgroup = one (head, 128-query block) = 2 wave64s x 64 queries, one wave per
+// SIMD; K/V tiles of 32 keys reach LDS by direct buffer->LDS copies into 4-slot rings; S^T = K Q^T and O^T += V^T P^T
+// on v_mfma_f32_32x32x16_bf16 so each lane owns one query row; the softmax keeps a fixed reference per row (see the
+// kernel's comment). fp32 (the parity lane): 4 wave64s x 32 queries on v_mfma_f32_32x32x2_f32 with a lazy
+// online-softmax rescale. Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of (head, query
+// block) items: adjacent query blocks select overlapping key blocks, so K/V tiles hit in L2.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace fvsr {
@@ -28,6 +26,8 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) char lds_char;
 
 // 3-input max without the NaN-quieting canonicalisation the compiler wraps around fmaxf (inputs are MFMA results
 // or -inf, never NaN)
@@ -60,201 +60,447 @@ __device__ __forceinline__ float rescale_if_grown(float mxc, float& m_run, float
 // ------------------------------------------------------------------------------------------------------------
 // bf16
 // ------------------------------------------------------------------------------------------------------------
+// One workgroup = one (head, 128-query block) = 2 wave64s x 64 queries, one wave per SIMD (up to 512 registers),
+// two workgroups per CU. Each wave holds its 64 queries as two 32-query groups; every K or V operand it reads from
+// LDS feeds two MFMAs (one per group), so LDS supplies one byte per 64 FLOP.
+//
+// Keys stream in tiles of 32 (a quarter of a 128-key block). K and V tiles land in two LDS rings of kSlots slots by
+// buffer_load ... lds (16 B per lane, no VGPR staging); a tile's rows are 256 B (one head) with the 16-byte chunks
+// XOR-swizzled by row so the ds_read_b128 (K) and ds_read_b64_tr_b16 (V^T) operand reads are bank-conflict free.
+// K of tile T+5 and V of tile T+3 are requested while tile T is processed: every copy has 4 tile steps to land.
+//
+// Softmax with a fixed reference per query row: Q is prescaled by log2(e)/sqrt(128) and one extra rank-2 MFMA step
+// per tile adds -m (the row's reference, the exact max of its first tile) and -2^100 for keys of the tile that do
+// not take part (ragged end, unselected block of the dense walk), so P = exp2(S^T) straight from the accumulators.
+// The largest partial row sum is tracked; a row whose scores outgrow the reference by 2^32, or underflow, makes the
+// workgroup redo its rows exactly (row-max pass, then attention with that max). The result is the softmax whatever
+// the reference is.
+//
+// Software pipeline per wave, step T: the exponentials of S(T) are issued between the MFMAs of PV(T-1) and QK(T+1),
+// so the VALU work hides under matrix-core time. The walk is unrolled by one 128-key block (4 steps); block indices
+// are read three blocks ahead so no scalar load latency sits on the step.
+namespace {
+
+constexpr int kTileKeys = 32;
+constexpr int kRowBytes = kHeadDim * 2;                // one head of one token, bf16
+constexpr int kTileBytes = kTileKeys * kRowBytes;      // 8 KB
+constexpr int kSlots = 4;                              // per ring: slot of tile T = T mod 4 = its quarter of the block
+constexpr int kVRing = kSlots * kTileBytes;            // byte offset of the V ring
+constexpr int kDmaPerStep = 8;                         // per wave and step: 4 K + 4 V loads of 1 KB
+constexpr float kMaskedScore = -1.2676506e30f;         // -2^100: exp2 of a masked key is exactly 0
+
+// 16-byte chunk swizzles. K: the 8 (or 16) lanes one ds_read_b128 cycle serves read 8 (16) consecutive rows of one
+// chunk -> distinct positions. V: a ds_read_b64_tr_b16 16-lane group reads 4 consecutive rows (a multiple of 4
+// apart) x 2 adjacent chunks -> 4 distinct chunk pairs.
+__device__ __forceinline__ int swz_k(int r) { return r & 15; }
+__device__ __forceinline__ int swz_v(int r) { return (r << 1) & 15; }
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+#define FVSR_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | (7 << 4))
+
+// 16 bytes per lane from a buffer straight into LDS at lds_base + OFF + 16 * lane. Issued as inline assembly so the
+// compiler does not order every later LDS read behind it: the kernel orders the copies itself (vmcnt + barrier).
+// M0 is written without a clobber declaration (the compiler reserves it); nothing else in these kernels uses M0. It
+// is loaded with s_mov_b32 from an address computed outside the asm (an s_add_u32 into M0 fed the copy a wrong
+// address on gfx950).
+template <int OFF>
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_base, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_base + OFF), "v"(voff),
+               "s"(rsrc), "s"(soff));
+}
+
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+
+}  // namespace
+
 template <bool DENSE>
-__global__ __launch_bounds__(256, 2) void attn_bf16_kernel(AttnArgs a) {
-  constexpr int BK = 64;                        // keys per tile
-  // Padded LDS rows (16 B of pad for K, 32 B for V) instead of an XOR swizzle: every MFMA operand address is then
-  // a per-lane base plus an immediate offset (few address registers), and the access patterns stay conflict-free:
-  //   K (ds_read_b128): 16 lanes read one 16-B column of 16 consecutive rows; 272 B = 68 dwords = 4 banks apart.
-  //   V (ds_read_b64_tr_b16): a 16-lane group reads 4 rows x 2 chunks x 2 halves; with 288 B = 72 dwords per row
-  //   the 32 dwords land in 8*row + 4*chunk + 2*half + {0, 1}: all distinct.
-  constexpr int KST = 272, VST = 288;
-  constexpr int TILE_K = BK * KST, TILE_V = BK * VST, STAGE = TILE_K + TILE_V;
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];   // [stage][K, V]
+__global__ __attribute__((amdgpu_flat_work_group_size(128, 128), amdgpu_waves_per_eu(1, 1)))
+void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_t* __restrict__ kcnt,
+                      const uint8_t* __restrict__ sel, const bf16* __restrict__ Q, bf16* __restrict__ O) {
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kVRing];
 
   const int lid = xcd_remap(blockIdx.x, gridDim.x);
   const int h = lid / a.nq, qb = lid - h * a.nq;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int hc = h * kHeadDim;
-  const bf16* __restrict__ Q = (const bf16*)a.q;
-  bf16* __restrict__ O = (bf16*)a.o;
   const int row_id = h * a.nq + qb;
-  const int cnt = a.kcnt[row_id];
+  const int cnt = kcnt[row_id];
 
   if (cnt <= 0) {   // empty query block -> zeros (SparseAttention.swift:47-53; DiT.swift:300-304)
-    for (int e = tid; e < kBlock * 16; e += 256) {
+    for (int e = tid; e < kBlock * 16; e += 128) {
       const int64_t row = (int64_t)qb * kBlock + (e >> 4);
       if (row < a.lq) *(u32x4*)(O + row * a.ld + hc + (e & 15) * 8) = u32x4{0, 0, 0, 0};
     }
     return;
   }
-  const int32_t* __restrict__ klist = a.kidx + (int64_t)row_id * a.nk_stride;
-  const uint8_t* __restrict__ srow = DENSE ? a.sel + (int64_t)row_id * a.nk : nullptr;
+  const int32_t* __restrict__ klist = kidx + (int64_t)row_id * a.nk_stride;
+  const uint8_t* __restrict__ srow = DENSE ? sel + (int64_t)row_id * a.nk : nullptr;
   const int nblocks = DENSE ? a.nk : min(cnt, a.nk_stride);
-  const int ntiles = nblocks * 2;
-  // keys of logical block j in tile half `half` that exist; a listed index outside [0, nk) contributes nothing
-  auto valid_keys = [&](int j, int half) -> int {
-    return (unsigned)j < (unsigned)a.nk ? (int)min<int64_t>(BK, a.lk - ((int64_t)j * kBlock + half * BK)) : 0;
-  };
 
-  // Q as the B operand: lane (query l32, k-half g) holds dims 16t + 8g .. +7 for t = 0..7.
-  const int64_t qrow = (int64_t)qb * kBlock + wave * 32 + l32;
-  bf16x8 qreg[8];
+  // Q as the B operand of S^T = K Q^T, prescaled by c: group q holds queries qb*128 + 64*wave + 32*q + l32,
+  // lane (query, k-half g) dims 16t + 8g .. +7
+  bf16x8 qop[2][8];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    if (qrow < a.lq) qreg[t] = *(const bf16x8*)(Q + qrow * a.ld + hc + 16 * t + 8 * g);
-    else qreg[t] = bf16x8{};
-  }
-
-  // K/V tiles through buffer loads: the resource spans the physical rows, so any row past it reads back as zero
-  // (the ragged last block needs no per-lane guard); the tile base goes in the scalar offset.
-  const uint32_t row_bytes = (uint32_t)a.ld * 2;
-  const int32_t range = (int32_t)(a.kv_rows * row_bytes);
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)a.k, 0, range, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.v, 0, range, 0x00020000);
-  const int ld_row = tid >> 4, ld_chunk = tid & 15;          // thread -> (row p*16 + tid/16, 16-byte chunk)
-  const int voff = ld_row * (int)row_bytes + hc * 2 + ld_chunk * 16;
-  u32x4 kreg[4], vreg[4];
-  auto load_tile = [&](int T) {
-    const int jj = T >> 1, half = T & 1;
-    const int j = DENSE ? jj : klist[jj];
-    if (valid_keys(j, half) > 0) {
-      const int soff = (int)((a.map.row(j) + half * BK) * row_bytes);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        kreg[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, voff, soff + p * 16 * (int)row_bytes, 0));
-        vreg[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, soff + p * 16 * (int)row_bytes, 0));
-      }
-    } else {
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        kreg[p] = u32x4{0, 0, 0, 0};
-        vreg[p] = u32x4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto store_tile = [&](int st) {
-    char* ks = smem + st * STAGE + ld_row * KST + ld_chunk * 16;
-    char* vs = smem + st * STAGE + TILE_K + ld_row * VST + ld_chunk * 16;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      *(u32x4*)(ks + p * 16 * KST) = kreg[p];
-      *(u32x4*)(vs + p * 16 * VST) = vreg[p];
-    }
-  };
-
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  f32x16 acc_o[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) acc_o[d] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
-  const float c = a.c;
-  // ds_read_tr addressing for the V^T operand (see file header): 16-lane group G, member m reads
-  // V[16u + 4(G/2) + m/4 (+8)][32dt + 16(G%2) + 4(m%4) .. +3]
-  const int G = lane >> 4, m = lane & 15;
-  const int tr_base = (4 * (G >> 1) + (m >> 2)) * VST + (2 * (G & 1) + ((m & 3) >> 1)) * 16 + (m & 1) * 8;
-  const int k_base = l32 * KST + g * 16;                       // K operand: row l32 (+32), chunk 2t + g
-  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
-
-  for (int T = 0; T < ntiles; ++T) {
-    const int st = T & 1;
-    const bool has_next = T + 1 < ntiles;
-    if (has_next) load_tile(T + 1);
-    const char* ks = smem + st * STAGE + k_base;
-    const char* vs = smem + st * STAGE + TILE_K + tr_base;
-
-    // S^T (64 keys x 32 queries) = K (64 x 128) . Q^T (128 x 32)
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
+  for (int q = 0; q < 2; ++q) {
+    const int64_t qrow = (int64_t)qb * kBlock + wave * 64 + q * 32 + l32;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const bf16x8 k0 = *(const bf16x8*)(ks + t * 32);
-      const bf16x8 k1 = *(const bf16x8*)(ks + 32 * KST + t * 32);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k0, qreg[t], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k1, qreg[t], s1, 0, 0, 0);
+      bf16x8 x = bf16x8{};
+      if (qrow < a.lq) x = *(const bf16x8*)(Q + qrow * a.ld + hc + 16 * t + 8 * g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (bf16)((float)x[e] * a.c);
+      // Q is only ever an MFMA operand: keep it in AGPRs, leaving the VGPRs to S, P and the LDS operands
+      asm volatile("" : "+a"(x));
+      qop[q][t] = x;
     }
-
-    // mask: unselected block (dense walk) or keys past the logical end (ragged last block); uniform branches
-    const int jj = T >> 1;
-    const int j = DENSE ? jj : klist[jj];
-    const int valid = (DENSE && srow[jj] == 0) ? 0 : valid_keys(j, T & 1);
-    if (valid < BK) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
-        if (kk >= valid) s0[r] = -INFINITY;
-        if (kk + 32 >= valid) s1[r] = -INFINITY;
-      }
-    }
-
-    // online softmax in the log2 domain; this lane's query row is l32
-    float mx0 = vmax3(s0[0], s0[1], s0[2]), mx1 = vmax3(s1[0], s1[1], s1[2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) {
-      mx0 = vmax3(mx0, s0[r], s0[r + 1]);
-      mx1 = vmax3(mx1, s1[r], s1[r + 1]);
-    }
-    const float mx = pair_max(vmax3(mx0, mx1, fmaxf(s0[15], s1[15])));
-    const float m_use = rescale_if_grown<4>(mx * c, m_run, l_run, acc_o);
-
-    // P = exp2(S c - m) packed to bf16 (the B operand of the PV product); the row sum is taken over the same
-    // bf16-rounded P with v_dot2 (two keys per instruction)
-    bf16x8 pop[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const f32x16& sp = (u >> 1) ? s1 : s0;
-      const int hh = u & 1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pop[u][e] = (bf16)__builtin_amdgcn_exp2f(fmaf(sp[8 * hh + e], c, -m_use));
-    }
-    float ls0 = 0.f, ls1 = 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      ls0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pop[u], pop[u], 0, 1), ones, ls0, false);
-      ls1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pop[u], pop[u], 2, 3), ones, ls1, false);
-      ls0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pop[u], pop[u], 4, 5), ones, ls0, false);
-      ls1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pop[u], pop[u], 6, 7), ones, ls1, false);
-    }
-    l_run += ls0 + ls1;
-
-    // O^T (128 dims x 32 queries) += V^T (128 x 64 keys) . P^T (64 x 32), 4 k-steps of 16 keys
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const char* pa = vs + 16 * u * VST + dt * 64;
-        const char* pb = pa + 8 * VST;
-        const i16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
-        const i16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pb);
-        // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword duplicated)
-        const i16x8 vcat = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vcat), pop[u], acc_o[dt], 0,
-                                                           0, 0);
-      }
-    }
-
-    if (has_next) store_tile(st ^ 1);
-    __syncthreads();
   }
 
-  const float l_tot = pair_sum(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qrow < a.lq) {
-    bf16* orow = O + qrow * a.ld + hc;
+  // tile loads: the buffer spans the physical K/V rows; a row past it reads as 0, so a ragged last block, a listed
+  // index outside [0, nk) and the tiles past the end of the walk load zeros without per-lane guards
+  const uint32_t row_bytes = (uint32_t)a.ld * 2;
+  const uint32_t range = (uint32_t)(a.kv_rows * row_bytes);
+  const u32x4 krs = buffer_rsrc(a.k, range), vrs = buffer_rsrc(a.v, range);
+  // a DMA load writes 1 KB of LDS (lane i -> bytes 16i..16i+15) = 4 rows; wave w fills rows 16w .. 16w+15
+  int voff_k[4], voff_v[4];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+  for (int p = 0; p < 4; ++p) {
+    const int r = wave * 16 + 4 * p + (lane >> 4), pos = lane & 15;
+    voff_k[p] = r * (int)row_bytes + hc * 2 + ((pos ^ swz_k(r)) << 4);
+    voff_v[p] = r * (int)row_bytes + hc * 2 + ((pos ^ swz_v(r)) << 4);
+  }
+  const uint32_t smem_lds = lds_addr(smem);
+  const uint32_t dma_base = smem_lds + wave * 16 * kRowBytes;
+  // buffer byte offset of block j's first row (j outside [0, nk): past the buffer -> zeros)
+  auto block_soff = [&](int j) -> int {
+    return (unsigned)j < (unsigned)a.nk ? (int)(a.map.row(j) * row_bytes) : (int)range;
+  };
+  const int sub_bytes = kTileKeys * (int)row_bytes;   // 32 rows
+  // K / V of quarter SUB of the block at soff into ring slot SLOT
+  auto issue_k = [&](auto slot_c, int soff) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    dma16<SLOT * kTileBytes + 0 * 4 * kRowBytes>(krs, dma_base, voff_k[0], soff);
+    dma16<SLOT * kTileBytes + 1 * 4 * kRowBytes>(krs, dma_base, voff_k[1], soff);
+    dma16<SLOT * kTileBytes + 2 * 4 * kRowBytes>(krs, dma_base, voff_k[2], soff);
+    dma16<SLOT * kTileBytes + 3 * 4 * kRowBytes>(krs, dma_base, voff_k[3], soff);
+  };
+  auto issue_v = [&](auto slot_c, int soff) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    dma16<kVRing + SLOT * kTileBytes + 0 * 4 * kRowBytes>(vrs, dma_base, voff_v[0], soff);
+    dma16<kVRing + SLOT * kTileBytes + 1 * 4 * kRowBytes>(vrs, dma_base, voff_v[1], soff);
+    dma16<kVRing + SLOT * kTileBytes + 2 * 4 * kRowBytes>(vrs, dma_base, voff_v[2], soff);
+    dma16<kVRing + SLOT * kTileBytes + 3 * 4 * kRowBytes>(vrs, dma_base, voff_v[3], soff);
+  };
+  // walked block b: buffer offset of its first row (past the buffer past the end of the walk) and its keys taking
+  // part (0 if unselected in the dense walk or outside [0, nk); else up to 128, fewer for a ragged last block)
+  auto walk_soff = [&](int b) -> int { return b < nblocks ? block_soff(DENSE ? b : klist[b]) : (int)range; };
+  auto walk_keys = [&](int b) -> int {
+    if (b >= nblocks) return 0;
+    const int j = DENSE ? b : klist[b];
+    if ((unsigned)j >= (unsigned)a.nk || (DENSE && srow[b] == 0)) return 0;
+    return (int)min<int64_t>(kBlock, a.lk - (int64_t)j * kBlock);
+  };
+  auto sub_valid = [&](int keys, int sub) -> int { return min(max(keys - sub * kTileKeys, 0), kTileKeys); };
+
+  // LDS operand addresses within a slot. K: row l32, chunk 2t+g. V^T (ds_read_b64_tr_b16): 16-lane group G, member
+  // mm reads row 16u + 8ab + 4(G/2) + mm/4, bf16 columns 32dt + 16(G%2) + 4(mm%4) .. +3.
+  int k_off[8], v_off[4];
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        bf16x4 ov;
-        ov[0] = (bf16)(acc_o[dt][4 * r4 + 0] * inv);
-        ov[1] = (bf16)(acc_o[dt][4 * r4 + 1] * inv);
-        ov[2] = (bf16)(acc_o[dt][4 * r4 + 2] * inv);
-        ov[3] = (bf16)(acc_o[dt][4 * r4 + 3] * inv);
-        *(bf16x4*)(orow + 32 * dt + 8 * r4 + 4 * g) = ov;
+  for (int t = 0; t < 8; ++t) k_off[t] = l32 * kRowBytes + (((2 * t + g) ^ swz_k(l32)) << 4);
+  const int G = lane >> 4, mm = lane & 15;
+  const int vr = 4 * (G >> 1) + (mm >> 2);   // + 16u + 8ab: the swizzle depends on the row mod 8 only
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+    v_off[dt] = vr * kRowBytes + (((4 * dt + 2 * (G & 1) + ((mm & 3) >> 1)) ^ swz_v(vr)) << 4) + (mm & 1) * 8;
+
+  f32x16 acc[2][4];
+  float l_run[2], m_row[2], part_max[2];
+  // the extra MFMA step: A lane (key l32, g = 0) holds k-slots {1, masked}, B lane (query, g = 0) {-m, -2^100}
+  bf16x8 bext[2];
+  auto set_ref = [&](int q, float m) {
+    bf16x8 b = bf16x8{};
+    if (g == 0) {
+      b[0] = (bf16)(-m);
+      b[1] = (bf16)kMaskedScore;
+    }
+    bext[q] = b;
+  };
+  auto aext = [&](int valid) -> bf16x8 {
+    bf16x8 x = bf16x8{};
+    if (g == 0) {
+      x[0] = (bf16)1.0f;
+      x[1] = l32 >= valid ? (bf16)1.0f : (bf16)0.0f;
+    }
+    return x;
+  };
+  lds_char* const lds = (lds_char*)(uintptr_t)smem_lds;
+  // S^T = K Q^T - m (keys that do not take part: - 2^100) for both groups, K from ring slot SLOT
+  auto qk = [&](auto slot_c, int valid, f32x16 (&s)[2]) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    bf16x8 kk[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) kk[t] = *(const lds_bf16x8*)(lds + SLOT * kTileBytes + k_off[t]);
+    const bf16x8 ax = aext(valid);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[t], qop[q][t], s[q], 0, 0, 0);
+  };
+  // O^T += V^T P^T, V from ring slot SLOT
+  auto pv = [&](auto slot_c, const bf16x8 (&p)[2][2]) {
+    constexpr int SLOT = decltype(slot_c)::value;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        lds_char* const pa = lds + kVRing + SLOT * kTileBytes + v_off[dt] + 16 * u * kRowBytes;
+        const i16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
+        const i16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pa + 8 * kRowBytes));
+        // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword duplicated)
+        const bf16x8 vv = __builtin_bit_cast(bf16x8, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          acc[q][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p[q][u], acc[q][dt], 0, 0, 0);
       }
+  };
+  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+  // P = exp2(S^T) packed to bf16 (u-th 16-key step = accumulator entries 8u .. 8u+7); partial row sum over the same
+  // bf16-rounded values
+  auto expo = [&](const f32x16& s, bf16x8 (&p)[2]) -> float {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[u][e] = (bf16)__builtin_amdgcn_exp2f(s[8 * u + e]);
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 0, 1), ones, s0, false);
+      s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 2, 3), ones, s1, false);
+      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 4, 5), ones, s0, false);
+      s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 6, 7), ones, s1, false);
+    }
+    return s0 + s1;
+  };
+  auto row_max = [&](const f32x16& s) -> float {
+    float mx = vmax3(s[0], s[1], s[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = vmax3(mx, s[r], s[r + 1]);
+    return pair_max(fmaxf(mx, s[15]));
+  };
+  // all of this wave's copies but the last `keep` steps' have landed, and every wave is past its LDS reads
+  auto sync_steps = [&](int keep) {
+    if (keep >= 2) FVSR_WAIT_VM_LGKM0(2 * kDmaPerStep);
+    else if (keep == 1) FVSR_WAIT_VM_LGKM0(kDmaPerStep);
+    else FVSR_WAIT_VM_LGKM0(0);
+    __builtin_amdgcn_s_barrier();
+  };
+  constexpr float kNoKey = -1e29f;   // a row max below this saw masked keys only
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C3 = std::integral_constant<int, 3>;
+
+  // One pass over the key tiles. MODE 0 (main): the reference m := the exact row max of the first tile (0 if it
+  // has no valid key), then P = exp2(S - m); the largest partial row sum is tracked. MODE 1: row max only. MODE 2:
+  // attention with m fixed to the exact row max.
+  // Step T (tile T = 4b + sub, ring slot = sub): request K(T+4) and V(T+2); S(T+1) = QK(T+1); O += PV(T-1);
+  // exponentials of S(T); then K(T+2) and V(T) must have landed (requested at step T-2).
+  auto run = [&](auto mode_c) {
+    constexpr int MODE = decltype(mode_c)::value;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      l_run[q] = 0.f;
+      part_max[q] = 0.f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) acc[q][d] = f32x16{};
+      set_ref(q, MODE == 2 ? m_row[q] : 0.f);
+      if (MODE == 1) m_row[q] = kMaskedScore;
+    }
+    f32x16 sA[2], sB[2];
+    bf16x8 pA[2][2], pB[2][2];
+    // per walked block: first-row buffer offset and keys taking part, read two blocks ahead of use
+    int o0 = walk_soff(0), o1 = walk_soff(1), o2 = walk_soff(2);
+    int n0 = walk_keys(0), n1 = walk_keys(1), n2 = walk_keys(2);
+    if (MODE == 0 && DENSE) {
+      // the reference comes from the tile the sparse walk starts with (the first tile of the first listed block),
+      // so both walks do the same arithmetic on every selected tile and agree bit for bit
+      const int jr = klist[0];
+      issue_k(C0{}, block_soff(jr));
+      FVSR_WAIT_VM_LGKM0(0);
+      __builtin_amdgcn_s_barrier();
+      qk(C0{}, (unsigned)jr < (unsigned)a.nk ? sub_valid((int)min<int64_t>(kBlock, a.lk - (int64_t)jr * kBlock), 0)
+                                             : 0,
+         sA);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float mx = row_max(sA[q]);
+        set_ref(q, (float)(bf16)(mx > kNoKey ? mx : 0.f));
+      }
+      __builtin_amdgcn_s_barrier();   // every wave is done with K slot 0 before the walk refills it
+    }
+    // prologue = virtual steps -4 .. -1: K(0..3) and V(-2..1); V(-2), V(-1) are zeros, so step 0's PV of the
+    // (zero) previous P adds exact zeros
+    issue_k(C0{}, o0);                issue_v(C2{}, (int)range);
+    issue_k(C1{}, o0 + sub_bytes);    issue_v(C3{}, (int)range);
+    issue_k(C2{}, o0 + 2 * sub_bytes); issue_v(C0{}, o0);
+    issue_k(C3{}, o0 + 3 * sub_bytes); issue_v(C1{}, o0 + sub_bytes);
+    sync_steps(3);   // K(0) landed
+    qk(C0{}, sub_valid(n0, 0), sA);
+    if (MODE == 0 && !DENSE) {
+      // reference = the exact row max of tile 0; the tile is then recomputed with it inside the accumulator, the
+      // same arithmetic as every later tile (and as the dense walk)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float mx = row_max(sA[q]);
+        set_ref(q, (float)(bf16)(mx > kNoKey ? mx : 0.f));
+      }
+      qk(C0{}, sub_valid(n0, 0), sA);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) pB[q][u] = bf16x8{};
+    sync_steps(2);   // K(1), V(-1) landed
+
+    // step with tile T in ring slot SUB: K(T+4) -> slot SUB, V(T+2) -> slot SUB+2, QK(T+1) <- K slot SUB+1,
+    // PV(T-1) <- V slot SUB+3 (all mod 4)
+    auto step = [&](auto sub_c, int valid_next, int soff_k, int soff_v, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
+                    bf16x8 (&p_prev)[2][2], bf16x8 (&p_cur)[2][2]) {
+      constexpr int SUB = decltype(sub_c)::value;
+      issue_k(std::integral_constant<int, SUB>{}, soff_k);
+      issue_v(std::integral_constant<int, (SUB + 2) & 3>{}, soff_v);
+      if (MODE == 1) {
+        qk(std::integral_constant<int, (SUB + 1) & 3>{}, valid_next, s_nxt);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) m_row[q] = fmaxf(m_row[q], row_max(s_cur[q]));
+      } else {
+        // Nine rounds, each fenced so the order below is the issue order: round r = MFMA r of QK(T+1) for both
+        // query groups (r = 0: the reference / mask step), the PV(T-1) MFMA pair r (r < 8) and one eighth of the
+        // exponentials of S(T). The two dependent QK chains see 3 other MFMAs between their links, and the VALU
+        // work sits between MFMAs.
+        lds_char* const vbase = lds + kVRing + ((SUB + 3) & 3) * kTileBytes;
+        lds_char* const kbase = lds + ((SUB + 1) & 3) * kTileBytes;
+        i16x4 va[8], vb[8];
+        bf16x8 kk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {   // operand reads in the order the rounds consume them
+          lds_char* const pa = vbase + v_off[j & 3] + 16 * (j >> 2) * kRowBytes;
+          va[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
+          vb[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pa + 8 * kRowBytes));
+          kk[j] = *(const lds_bf16x8*)(kbase + k_off[j]);
+        }
+        const bf16x8 ax = aext(valid_next);
+        float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+        for (int r = 0; r < 9; ++r) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            s_nxt[q] = r == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0)
+                              : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[r - 1], qop[q][r - 1], s_nxt[q], 0, 0, 0);
+          if (r < 8) {
+            // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword
+            // duplicated)
+            const bf16x8 vv =
+                __builtin_bit_cast(bf16x8, __builtin_shufflevector(va[r], vb[r], 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+              acc[q][r & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p_prev[q][r >> 2], acc[q][r & 3], 0, 0, 0);
+            // exponentials of S(T) entries 4h .. 4h+3 of 16-key step u, group q
+            const int q = r >> 2, u = (r >> 1) & 1, h = r & 1;
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+              bf16x2 pr;
+              pr[0] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e]);
+              pr[1] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e + 1]);
+              p_cur[q][u][4 * h + e] = pr[0];
+              p_cur[q][u][4 * h + e + 1] = pr[1];
+              sum[q][e >> 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, sum[q][e >> 1], false);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float part = sum[q][0] + sum[q][1];
+          l_run[q] += part;
+          if (MODE == 0) part_max[q] = fmaxf(part_max[q], part);
+        }
+      }
+      // keep every instruction of this step on its side of the barrier
+      __builtin_amdgcn_sched_barrier(0);
+      sync_steps(2);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int b = 0; b < nblocks; ++b) {
+      const int o3 = walk_soff(b + 3), n3 = walk_keys(b + 3);
+      // step 4b+s: QK tile 4b+s+1, K tile 4b+s+4 (block b+1), V tile 4b+s+2
+      step(C0{}, sub_valid(n0, 1), o1, o0 + 2 * sub_bytes, sA, sB, pB, pA);
+      step(C1{}, sub_valid(n0, 2), o1 + sub_bytes, o0 + 3 * sub_bytes, sB, sA, pA, pB);
+      step(C2{}, sub_valid(n0, 3), o1 + 2 * sub_bytes, o1, sA, sB, pB, pA);
+      step(C3{}, sub_valid(n1, 0), o1 + 3 * sub_bytes, o1 + sub_bytes, sB, sA, pA, pB);
+      o0 = o1; o1 = o2; o2 = o3;
+      n0 = n1; n1 = n2; n2 = n3;
+    }
+    if (MODE != 1) pv(C3{}, pB);   // PV of the last tile (4 * nblocks - 1, slot 3)
+    // drain the zero-fill copies requested past the end before LDS is reused
+    FVSR_WAIT_VM_LGKM0(0);
+    __builtin_amdgcn_s_barrier();
+  };
+
+  run(std::integral_constant<int, 0>{});
+  // rows whose scores outgrew the first-tile reference by 2^32, or whose exponentials all underflowed: redo the
+  // workgroup exactly (row max pass, then attention with that max); workgroup-uniform so the barriers match
+  {
+    bool bad = false;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float pm = pair_max(part_max[q]);
+      bad |= !(pm <= 4294967296.f) || pm < 2.3283064e-10f;
+    }
+    int* flag = (int*)smem;
+    if (tid == 0) flag[0] = 0;
+    __syncthreads();
+    if (__ballot(bad) != 0 && lane == 0) flag[0] = 1;
+    __syncthreads();
+    const bool redo = flag[0] != 0;
+    __syncthreads();
+    if (redo) {
+      run(std::integral_constant<int, 1>{});
+#pragma unroll
+      for (int q = 0; q < 2; ++q) m_row[q] = (float)(bf16)(m_row[q] > kNoKey ? m_row[q] : 0.f);
+      run(std::integral_constant<int, 2>{});
+    }
+  }
+
+  const float l0 = pair_sum(l_run[0]), l1 = pair_sum(l_run[1]);
+  const float inv0 = l0 > 0.f ? 1.f / l0 : 0.f, inv1 = l1 > 0.f ? 1.f / l1 : 0.f;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int64_t qrow = (int64_t)qb * kBlock + wave * 64 + q * 32 + l32;
+    const float inv = q ? inv1 : inv0;
+    if (qrow < a.lq) {
+      bf16* orow = O + qrow * a.ld + hc;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          bf16x4 ov;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ov[e] = (bf16)(acc[q][dt][4 * r4 + e] * inv);
+          *(bf16x4*)(orow + 32 * dt + 8 * r4 + 4 * g) = ov;
+        }
+    }
   }
 }
 
@@ -481,8 +727,12 @@ int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t strea
   if (nwg <= 0) return FVSR_OK;
   dim3 grid(nwg), block(256);
   if (dtype == FVSR_DTYPE_BF16) {
-    if (dense) hipLaunchKernelGGL(attn_bf16_kernel<true>, grid, block, 0, stream, a);
-    else hipLaunchKernelGGL(attn_bf16_kernel<false>, grid, block, 0, stream, a);
+    if (dense)
+      hipLaunchKernelGGL(attn_bf16_kernel<true>, grid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                         (const bf16*)a.q, (bf16*)a.o);
+    else
+      hipLaunchKernelGGL(attn_bf16_kernel<false>, grid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                         (const bf16*)a.q, (bf16*)a.o);
   } else {
     if (dense) hipLaunchKernelGGL(attn_f32_kernel<true>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(attn_f32_kernel<false>, grid, block, 0, stream, a);
