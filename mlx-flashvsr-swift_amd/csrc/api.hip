@@ -46,7 +46,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // workspace carve for one select + attention call
 struct Carve {
-  size_t pq, pk, probs, kidx, kcnt, sel, total;
+  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, total;
 };
 static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   Carve c;
@@ -57,6 +57,8 @@ static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   c.kidx = off; off += align256((size_t)heads * nq * nk * 4);
   c.kcnt = off; off += align256((size_t)heads * nq * 4);
   c.sel = off; off += align256((size_t)heads * nq * nk);
+  c.order = off; off += align256((size_t)heads * nq * 4);
+  c.counter = off; off += 256;
   c.total = off;
   return c;
 }
@@ -246,7 +248,7 @@ int fvsr_lcsa_select(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const
 static AttnArgs make_args(const void* q, int64_t lq, const void* k, const void* v, int64_t lk, int heads,
                           const int32_t* kidx, const int32_t* kcnt, const uint8_t* sel, int nk_stride, int nk,
                           KeyMap map, void* o) {
-  AttnArgs a;
+  AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o;
   a.lq = lq; a.lk = lk;
   a.heads = heads; a.ld = heads * kHeadDim;
@@ -258,6 +260,16 @@ static AttnArgs make_args(const void* q, int64_t lq, const void* k, const void* 
   a.kv_rows = lk;
   a.c = (float)(1.4426950408889634 / std::sqrt((double)kHeadDim));
   return a;
+}
+
+// the persistent walk's row order and work counter, carved from the context workspace (grown if needed)
+static int attach_order(fvsr_ctx* ctx, AttnArgs& a, int64_t nk) {
+  const Carve cv = carve(a.heads, a.nq, nk, a.ld);
+  int rc = ensure_ws(ctx, cv.total);
+  if (rc) return rc;
+  a.order = (int32_t*)((char*)ctx->ws + cv.order);
+  a.counter = (int32_t*)((char*)ctx->ws + cv.counter);
+  return FVSR_OK;
 }
 
 static int check_attn_common(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
@@ -284,7 +296,8 @@ int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, con
   FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
   const int nk = (int)ceil_div(lk, kBlock);
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
-  const AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, KeyMap{0, 1, 1 << 30}, o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, KeyMap{0, 1, 1 << 30}, o);
+  if ((rc = attach_order(ctx, a, nk))) return rc;
   return launch_attention(dtype, false, a, (hipStream_t)stream);
 }
 
@@ -305,8 +318,8 @@ int fvsr_lcsa_attention_mask(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq
   hipStream_t st = (hipStream_t)stream;
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   if ((rc = launch_lists_from_mask(block_mask, (int)(heads * nq), (int)nk, kidx, kcnt, sel, st))) return rc;
-  const AttnArgs a =
-      make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, KeyMap{0, 1, 1 << 30}, o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, KeyMap{0, 1, 1 << 30}, o);
+  if ((rc = attach_order(ctx, a, nk))) return rc;
   return launch_attention(dtype, mode == FVSR_ATTN_DENSE, a, st);
 }
 
@@ -465,6 +478,8 @@ static int attention_ring_impl(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const 
   AttnArgs a = make_args(q, lq, r->layer_k(layer), r->layer_v(layer), (int64_t)nk * kBlock, r->heads, kidx, kcnt,
                          sel, nk_stride, nk, r->map(layer), o);
   a.kv_rows = (int64_t)r->layer_tokens();
+  int rc = attach_order(ctx, a, nk);
+  if (rc) return rc;
   return launch_attention(r->dtype, dense, a, stream);
 }
 

@@ -73,6 +73,8 @@ struct AttnArgs {
   KeyMap map;
   int64_t kv_rows;       // token rows physically present in the k/v buffers (buffer-load range)
   float c;               // softmax scale * log2(e)
+  int32_t* order;        // (H * nq) rows, longest key list first (bf16 persistent walk; workspace)
+  int32_t* counter;      // next index into `order` (workspace; zeroed by the order kernel)
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

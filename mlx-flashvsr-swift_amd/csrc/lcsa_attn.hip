@@ -10,6 +10,7 @@
 // kernel's comment). fp32 (the parity lane): 4 wave64s x 32 queries on v_mfma_f32_32x32x2_f32 with a lazy
 // online-softmax rescale. Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of (head, query
 // block) items: adjacent query blocks select overlapping key blocks, so K/V tiles hit in L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -124,16 +125,26 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 template <bool DENSE>
 __global__ __attribute__((amdgpu_flat_work_group_size(128, 128), amdgpu_waves_per_eu(1, 1)))
 void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_t* __restrict__ kcnt,
-                      const uint8_t* __restrict__ sel, const bf16* __restrict__ Q, bf16* __restrict__ O) {
+                      const uint8_t* __restrict__ sel, const bf16* __restrict__ Q, bf16* __restrict__ O,
+                      const int32_t* __restrict__ order, int32_t* __restrict__ counter) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kVRing];
+  __shared__ int item_s;
 
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int h = lid / a.nq, qb = lid - h * a.nq;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
+  const int rows = a.heads * a.nq;
+  // Persistent: the grid is sized to the resident workgroups; each takes the next row (head, query block) from the
+  // list ordered longest key list first, so the long rows start early and the short ones fill in behind them.
+  for (;;) {
+  if (tid == 0) item_s = atomicAdd(counter, 1);
+  __syncthreads();
+  const int item = item_s;
+  __syncthreads();
+  if (item >= rows) break;
+  const int row_id = order[item];
+  const int h = row_id / a.nq, qb = row_id - h * a.nq;
   const int hc = h * kHeadDim;
-  const int row_id = h * a.nq + qb;
   const int cnt = kcnt[row_id];
 
   if (cnt <= 0) {   // empty query block -> zeros (SparseAttention.swift:47-53; DiT.swift:300-304)
@@ -141,7 +152,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
       const int64_t row = (int64_t)qb * kBlock + (e >> 4);
       if (row < a.lq) *(u32x4*)(O + row * a.ld + hc + (e & 15) * 8) = u32x4{0, 0, 0, 0};
     }
-    return;
+    continue;
   }
   const int32_t* __restrict__ klist = kidx + (int64_t)row_id * a.nk_stride;
   const uint8_t* __restrict__ srow = DENSE ? sel + (int64_t)row_id * a.nk : nullptr;
@@ -502,6 +513,52 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         }
     }
   }
+  }   // next row
+}
+
+// Rows (head, query block) ordered by decreasing key-list length for the persistent bf16 walk, and its work counter
+// reset to 0. One workgroup: counting sort over min(listed blocks, 4095) (the dense walk: every non-empty row is a
+// full walk); rows of equal length keep no particular order (every row is computed independently).
+__global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
+                                                          int dense, int32_t* __restrict__ order,
+                                                          int32_t* __restrict__ counter) {
+  constexpr int kBins = 4096;
+  __shared__ int bin_start[kBins];
+  __shared__ int part[1024];
+  const int tid = threadIdx.x;
+  for (int b = tid; b < kBins; b += 1024) bin_start[b] = 0;
+  __syncthreads();
+  auto bin_of = [&](int r) -> int {   // bin 0 = the longest lists
+    const int c = kcnt[r];
+    const int len = c <= 0 ? 0 : (dense ? 1 : min(min(c, nk_stride), kBins - 1));
+    return kBins - 1 - len;
+  };
+  for (int r = tid; r < rows; r += 1024) atomicAdd(&bin_start[bin_of(r)], 1);
+  __syncthreads();
+  // exclusive scan of the 4096 bin counts: 4 bins per thread, then a scan of the 1024 thread sums
+  int v[4], sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = bin_start[4 * tid + i];
+    sum += v[i];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {
+    const int x = tid >= d ? part[tid - d] : 0;
+    __syncthreads();
+    part[tid] += x;
+    __syncthreads();
+  }
+  int run = part[tid] - sum;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bin_start[4 * tid + i] = run;
+    run += v[i];
+  }
+  __syncthreads();
+  for (int r = tid; r < rows; r += 1024) order[atomicAdd(&bin_start[bin_of(r)], 1)] = r;
+  if (tid == 0) *counter = 0;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -722,17 +779,35 @@ __global__ __launch_bounds__(256) void sel_from_lists_kernel(const int32_t* __re
 // ------------------------------------------------------------------------------------------------------------
 // launch
 // ------------------------------------------------------------------------------------------------------------
+// compute units of the current device (cached per device)
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t stream) {
   const int nwg = a.heads * a.nq;
   if (nwg <= 0) return FVSR_OK;
   dim3 grid(nwg), block(256);
   if (dtype == FVSR_DTYPE_BF16) {
+    if (!a.order || !a.counter) return set_error(FVSR_ERR_INVALID_ARG, "attention: no workspace for the row order");
+    hipLaunchKernelGGL(attn_order_kernel, dim3(1), dim3(1024), 0, stream, a.kcnt, nwg, a.nk_stride, dense ? 1 : 0,
+                       a.order, a.counter);
+    // two workgroups (64 KB of LDS, one wave per SIMD each) are resident per CU
+    const dim3 pgrid(std::min(nwg, 2 * device_cus()));
     if (dense)
-      hipLaunchKernelGGL(attn_bf16_kernel<true>, grid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
-                         (const bf16*)a.q, (bf16*)a.o);
+      hipLaunchKernelGGL(attn_bf16_kernel<true>, pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                         (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
     else
-      hipLaunchKernelGGL(attn_bf16_kernel<false>, grid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
-                         (const bf16*)a.q, (bf16*)a.o);
+      hipLaunchKernelGGL(attn_bf16_kernel<false>, pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                         (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
   } else {
     if (dense) hipLaunchKernelGGL(attn_f32_kernel<true>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(attn_f32_kernel<false>, grid, block, 0, stream, a);
