@@ -211,6 +211,15 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     dma16<kVRing + SLOT * kTileBytes + 2 * 4 * kRowBytes>(vrs, dma_base, voff_v[2], soff);
     dma16<kVRing + SLOT * kTileBytes + 3 * 4 * kRowBytes>(vrs, dma_base, voff_v[3], soff);
   };
+  // one of the 4 copies (rows 4P .. 4P+3 of this wave's half) of K / V into ring slot SLOT
+  auto dma_k = [&](auto slot_c, auto p_c, int soff) {
+    constexpr int SLOT = decltype(slot_c)::value, P = decltype(p_c)::value;
+    dma16<SLOT * kTileBytes + P * 4 * kRowBytes>(krs, dma_base, voff_k[P], soff);
+  };
+  auto dma_v = [&](auto slot_c, auto p_c, int soff) {
+    constexpr int SLOT = decltype(slot_c)::value, P = decltype(p_c)::value;
+    dma16<kVRing + SLOT * kTileBytes + P * 4 * kRowBytes>(vrs, dma_base, voff_v[P], soff);
+  };
   // walked block b: buffer offset of its first row (past the buffer past the end of the walk) and its keys taking
   // part (0 if unselected in the dense walk or outside [0, nk); else up to 128, fewer for a ragged last block)
   auto walk_soff = [&](int b) -> int { return b < nblocks ? block_soff(DENSE ? b : klist[b]) : (int)range; };
@@ -389,58 +398,93 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     auto step = [&](auto sub_c, int valid_next, int soff_k, int soff_v, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
                     bf16x8 (&p_prev)[2][2], bf16x8 (&p_cur)[2][2]) {
       constexpr int SUB = decltype(sub_c)::value;
-      issue_k(std::integral_constant<int, SUB>{}, soff_k);
-      issue_v(std::integral_constant<int, (SUB + 2) & 3>{}, soff_v);
+      using KS = std::integral_constant<int, SUB>;
+      using VS = std::integral_constant<int, (SUB + 2) & 3>;
       if (MODE == 1) {
+        issue_k(KS{}, soff_k);
+        issue_v(VS{}, soff_v);
         qk(std::integral_constant<int, (SUB + 1) & 3>{}, valid_next, s_nxt);
 #pragma unroll
         for (int q = 0; q < 2; ++q) m_row[q] = fmaxf(m_row[q], row_max(s_cur[q]));
       } else {
-        // Nine rounds, each fenced so the order below is the issue order: round r = MFMA r of QK(T+1) for both
-        // query groups (r = 0: the reference / mask step), the PV(T-1) MFMA pair r (r < 8) and one eighth of the
-        // exponentials of S(T). The two dependent QK chains see 3 other MFMAs between their links, and the VALU
-        // work sits between MFMAs.
+        // Nine rounds, each fenced so the order below is the issue order. Round 0: the reference / mask MFMA of
+        // QK(T+1) for both query groups and 8 exponentials of S(T), work that needs no LDS operand. Round r = 1..8:
+        // MFMA r of QK(T+1) for both groups, the PV(T-1) MFMA pair r-1 and (r <= 6) 4 more exponentials. Every
+        // round also requests the LDS operands of the round two ahead and (r < 8) one of the 8 buffer->LDS copies of
+        // this step, so no burst of memory instructions stalls the matrix core. The two dependent QK chains see 3
+        // other MFMAs between their links.
         lds_char* const vbase = lds + kVRing + ((SUB + 3) & 3) * kTileBytes;
         lds_char* const kbase = lds + ((SUB + 1) & 3) * kTileBytes;
         i16x4 va[8], vb[8];
         bf16x8 kk[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {   // operand reads in the order the rounds consume them
+        // operands of round j + 1: V^T pair j (PV) and K chunk j (QK)
+        auto read_ops = [&](int j) {
           lds_char* const pa = vbase + v_off[j & 3] + 16 * (j >> 2) * kRowBytes;
           va[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
           vb[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pa + 8 * kRowBytes));
           kk[j] = *(const lds_bf16x8*)(kbase + k_off[j]);
-        }
+        };
+        auto dma = [&](auto r_c) {
+          constexpr int R = decltype(r_c)::value;
+          if constexpr (R < 4) dma_k(KS{}, std::integral_constant<int, R>{}, soff_k);
+          else dma_v(VS{}, std::integral_constant<int, R - 4>{}, soff_v);
+        };
         const bf16x8 ax = aext(valid_next);
         float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+        // exponentials of S(T) entries 4h .. 4h+3 (pairs packed to bf16) of 16-key step u, group q; chunk c = 0..7
+        auto expo4 = [&](int c) {
+          const int q = c >> 2, u = (c >> 1) & 1, h = c & 1;
 #pragma unroll
-        for (int r = 0; r < 9; ++r) {
+          for (int e = 0; e < 4; e += 2) {
+            bf16x2 pr;
+            pr[0] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e]);
+            pr[1] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e + 1]);
+            p_cur[q][u][4 * h + e] = pr[0];
+            p_cur[q][u][4 * h + e + 1] = pr[1];
+            sum[q][e >> 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, sum[q][e >> 1], false);
+          }
+        };
+        auto round = [&](auto r_c) {
+          constexpr int r = decltype(r_c)::value;
+          if constexpr (r == 0) {
+            read_ops(0);
+            read_ops(1);
+          } else if constexpr (r + 1 < 8) {
+            read_ops(r + 1);
+          }
 #pragma unroll
           for (int q = 0; q < 2; ++q)
             s_nxt[q] = r == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0)
-                              : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[r - 1], qop[q][r - 1], s_nxt[q], 0, 0, 0);
-          if (r < 8) {
+                              : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[r == 0 ? 0 : r - 1], qop[q][r == 0 ? 0 : r - 1],
+                                                                        s_nxt[q], 0, 0, 0);
+          if constexpr (r >= 1) {
             // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword
             // duplicated)
+            constexpr int j = r - 1;
             const bf16x8 vv =
-                __builtin_bit_cast(bf16x8, __builtin_shufflevector(va[r], vb[r], 0, 1, 2, 3, 4, 5, 6, 7));
+                __builtin_bit_cast(bf16x8, __builtin_shufflevector(va[j], vb[j], 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
             for (int q = 0; q < 2; ++q)
-              acc[q][r & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p_prev[q][r >> 2], acc[q][r & 3], 0, 0, 0);
-            // exponentials of S(T) entries 4h .. 4h+3 of 16-key step u, group q
-            const int q = r >> 2, u = (r >> 1) & 1, h = r & 1;
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-              bf16x2 pr;
-              pr[0] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e]);
-              pr[1] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e + 1]);
-              p_cur[q][u][4 * h + e] = pr[0];
-              p_cur[q][u][4 * h + e + 1] = pr[1];
-              sum[q][e >> 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, sum[q][e >> 1], false);
-            }
+              acc[q][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p_prev[q][j >> 2], acc[q][j & 3], 0, 0, 0);
           }
+          if constexpr (r == 0) {
+            expo4(0);
+            expo4(1);
+          } else if constexpr (r <= 6) {
+            expo4(r + 1);
+          }
+          if constexpr (r < 8) dma(r_c);
           __builtin_amdgcn_sched_barrier(0);
-        }
+        };
+        round(C0{});
+        round(C1{});
+        round(C2{});
+        round(C3{});
+        round(std::integral_constant<int, 4>{});
+        round(std::integral_constant<int, 5>{});
+        round(std::integral_constant<int, 6>{});
+        round(std::integral_constant<int, 7>{});
+        round(std::integral_constant<int, 8>{});
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const float part = sum[q][0] + sum[q][1];
@@ -517,8 +561,9 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 }
 
 // Rows (head, query block) ordered by decreasing key-list length for the persistent bf16 walk, and its work counter
-// reset to 0. One workgroup: counting sort over min(listed blocks, 4095) (the dense walk: every non-empty row is a
-// full walk); rows of equal length keep no particular order (every row is computed independently).
+// reset to 0. One workgroup: counting sort over the list length in bins of 8 blocks (the dense walk: every
+// non-empty row is a full walk). Inside a bin rows come out close to row order (head-major, neighbouring query
+// blocks together), so the workgroups running at once share key blocks in L2; the order does not affect results.
 __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
                                                           int dense, int32_t* __restrict__ order,
                                                           int32_t* __restrict__ counter) {
@@ -530,7 +575,7 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
   __syncthreads();
   auto bin_of = [&](int r) -> int {   // bin 0 = the longest lists
     const int c = kcnt[r];
-    const int len = c <= 0 ? 0 : (dense ? 1 : min(min(c, nk_stride), kBins - 1));
+    const int len = c <= 0 ? 0 : (dense ? 1 : min(((min(c, nk_stride) + 7) >> 3), kBins - 1));
     return kBins - 1 - len;
   };
   for (int r = tid; r < rows; r += 1024) atomicAdd(&bin_start[bin_of(r)], 1);
