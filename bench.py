@@ -40,6 +40,11 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="time only the attention kernel loop (profiling)")
+    ap.add_argument("--stream", action="store_true",
+                    help="the streaming attention stack at 1920x1152 instead: 30 layers (KV ring per layer) over a "
+                         "6-latent-frame first chunk and 4 chunks of 2 latent frames; append + select + attention + "
+                         "evict per layer call; prints its own JSON line")
+    ap.add_argument("--layers", type=int, default=30)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain copy of known size (the window-partition kernel over 16x72x120 bf16 "
                          "tokens of 1536 channels: 424.7 MB read + 424.7 MB written per launch), the reference "
@@ -129,6 +134,89 @@ def copy_calibration(steps: int):
                                            "GB/s": round(2 * nbytes / ms / 1e6, 1)}}), flush=True)
 
 
+def stream_bench(args):
+    """The attention stack of the streaming DiT at 1920x1152 (the reference's geometry: s = 135 blocks per slice, a
+    first chunk of 6 latent frames = 3 slices, then chunks of 2 latent frames = 1 slice; KV window 3 slices;
+    default top-k 16199, local range 11; Pipeline.swift:22-23,68,95-102; DiT.swift:478-538). Each layer call runs
+    append + select + block-sparse attention + evict through fvsr_lcsa_layer. Q/K/V of each chunk are synthetic
+    (N(0,1), per-head RMS norm, 3-D RoPE at the chunk's latent frames), resident in HBM and shared by the layers."""
+    import torch
+
+    import fvsr_lcsa
+    from fvsr_lcsa import synth
+
+    dev = torch.device("cuda:0")
+    H, bh, bw = 12, 9, 15
+    s = bh * bw
+    lat_h, lat_w, C = 8 * bh, 8 * bw, H * 128
+    local = fvsr_lcsa.local_block_mask(bh, bw, 11)
+    topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
+    chunks = [(3, 0), (1, 6), (1, 8), (1, 10), (1, 12)]   # (slices, first latent frame)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    data = []
+    for n, t0 in chunks:
+        f = 2 * n
+        L = f * lat_h * lat_w
+        q, k, v = (torch.randn((L, C), generator=gen, device=dev) for _ in range(3))
+        cos, sin = synth.rope_grid(f, lat_h, lat_w, t0, device=dev)
+        q = synth.rope_apply(synth.rms_norm(q, H), H, cos, sin)
+        k = synth.rope_apply(synth.rms_norm(k, H), H, cos, sin)
+        data.append(tuple(synth.window_partition(x, f, lat_h, lat_w).to(torch.bfloat16).contiguous()
+                          for x in (q, k, v)))
+    ring = fvsr_lcsa.KVRing(args.layers, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    outs = [torch.empty_like(d[0]) for d in data]
+    # kept block pairs per chunk (untimed; the same data feeds every layer)
+    kept_pairs = []
+    for (n, _), (q, k, v), o in zip(chunks, data, outs):
+        _, m, _ = ring.layer_call(0, q, k, v, n, n, local, topk, out=o, want_mask=True)
+        kept_pairs.append(float(m.sum().item()))
+    ring.reset()
+
+    def run_stream(events=None):
+        ring.reset()
+        for c, ((n, _), (q, k, v), o) in enumerate(zip(chunks, data, outs)):
+            if events is not None:
+                events[c][0].record()
+            for layer in range(args.layers):
+                ring.layer_call(layer, q, k, v, n, n, local, topk, out=o)
+            if events is not None:
+                events[c][1].record()
+
+    for _ in range(max(1, args.warmup // 5)):
+        run_stream()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 10)
+    tot = [0.0] * len(chunks)
+    for _ in range(reps):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunks]
+        run_stream(ev)
+        torch.cuda.synchronize()
+        for c, (a0, a1) in enumerate(ev):
+            tot[c] += a0.elapsed_time(a1) / reps
+    flops = [4.0 * 128 ** 3 * p * args.layers for p in kept_pairs]
+    steady = tot[1:]
+    line = {
+        "metric": "LCSA attention stack per streaming chunk, 1920x1152 (append + select + attention + evict)",
+        "unit": "ms per chunk (all layers)",
+        "value": round(sum(steady) / len(steady), 3),
+        "higher_is_better": False,
+        "n_gpus": 1,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1), per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)",
+        "config": {"workload": "stream_1920x1152_bf16", "layers": args.layers, "heads": H, "head_dim": 128,
+                   "spatial_blocks_per_slice": s, "local_range": 11, "topk": topk, "kv_window_slices": 3,
+                   "chunks": [{"query_blocks": n * s, "key_blocks": min(n + (3 if c else 0), 4) * s}
+                              for c, (n, _) in enumerate(chunks)]},
+        "chunk_ms": [round(t, 3) for t in tot],
+        "per_layer_call_ms": [round(t / args.layers, 4) for t in tot],
+        "kept_block_fraction": [round(p / (H * n * s * min(n + (3 if c else 0), 4) * s), 4)
+                                for c, ((n, _), p) in enumerate(zip(chunks, kept_pairs))],
+        "effective_tflops_kept": [round(f / (t * 1e-3) / 1e12, 1) for f, t in zip(flops, tot)],
+        "reps": reps,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -143,6 +231,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.stream:
+        stream_bench(args)
         return
     dev = torch.device("cuda:0")
     wl = synth.WORKLOADS[args.workload]

@@ -12,10 +12,10 @@
 //   pool_kernel          one workgroup per 128-token block: coalesced 16-byte loads, fp32 sums, mean
 //   scores_softmax_kernel one workgroup per (8 query blocks, head): pooled-key rows read once per 8 query rows,
 //                         scores + local mask staged in LDS, one wave per row for max / exp / sum / normalise
-//   topk_emit_kernel     one 1024-thread workgroup per (head, query slice): exact k-th-largest by a 4 x 8-bit
+//   topk_threshold_kernel one 1024-thread workgroup per (head, query slice): exact (k+1)-th largest by a 4-pass
 //                         radix select over the fp32 bit patterns (probs are >= 0, so bit order = value order),
-//                         per-wave LDS histograms; then the mask, selection bytes and compacted key lists
-//                         (ballot + popcount) for every query row of the slice.
+//                         row held in registers, per-wave LDS histograms
+//   topk_emit_kernel     one wave per query row: mask, selection bytes and compacted key lists (ballot + popcount)
 #include "common.hpp"
 
 namespace fvsr {
@@ -133,13 +133,17 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
 // exact top-k threshold + mask / list emit
 // ------------------------------------------------------------------------------------------------------------
 constexpr int kTopkThreads = 1024;
+constexpr int kTopkRegs = 80;   // elements per thread kept in registers (rows up to 81920 entries)
 
-__global__ __launch_bounds__(kTopkThreads) void topk_emit_kernel(const float* __restrict__ probs, int nq, int nk,
-                                                                 int q_slices, int topk,
-                                                                 float* __restrict__ mask_out,
-                                                                 uint8_t* __restrict__ sel,
-                                                                 int32_t* __restrict__ kidx,
-                                                                 int32_t* __restrict__ kcnt) {
+// One 1024-thread workgroup per (head, query slice) row of s*Nk probs: the (k+1)-th largest, k = min(n-1, topk), by
+// an exact radix select over the fp32 bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0).
+// Digits follow the float layout — exponent [30:23], then mantissa [22:15], [14:7], [6:0] — so the first pass
+// spreads the row over its octaves. The row stays in registers across the passes (re-read from memory only for
+// rows longer than 1024 * kTopkRegs). Exact zeros (key blocks outside the local window) are counted with a wave
+// ballot instead of 64 colliding LDS atomics.
+__global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const float* __restrict__ probs, int nq,
+                                                                      int nk, int q_slices, int topk,
+                                                                      float* __restrict__ thr_out) {
   __shared__ unsigned hist[kTopkThreads / 64][256];
   __shared__ unsigned tot[256];
   __shared__ unsigned s_prefix, s_rank;
@@ -151,19 +155,44 @@ __global__ __launch_bounds__(kTopkThreads) void topk_emit_kernel(const float* __
   const unsigned* bits = (const unsigned*)(probs + base);
   const int64_t n = (int64_t)sq * nk;
   const int64_t k = min<int64_t>(n - 1, topk);
+  const bool in_regs = n <= (int64_t)kTopkThreads * kTopkRegs;
+  unsigned v[kTopkRegs];
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kTopkRegs; ++i) {
+      const int64_t e = (int64_t)i * kTopkThreads + tid;
+      v[i] = e < n ? bits[e] : 0xffffffffu;   // padding never matches a prefix (bit 31 set)
+    }
+  }
   unsigned rank = (unsigned)(n - 1 - k);            // ascending rank of the (k+1)-th largest
-  unsigned prefix = 0, pmask = 0;
+  unsigned prefix = 0, pmask = 0x80000000u;
   if (tid == 0) {
     s_prefix = 0;
     s_rank = rank;
   }
-  for (int shift = 24; shift >= 0; shift -= 8) {
+  const int shifts[4] = {23, 15, 7, 0};
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = shifts[pass];
+    const unsigned dmask = pass == 3 ? 127u : 255u;
     for (int e = tid; e < (kTopkThreads / 64) * 256; e += kTopkThreads) (&hist[0][0])[e] = 0;
     __syncthreads();
-    for (int64_t e = tid; e < n; e += kTopkThreads) {
-      const unsigned u = bits[e];
-      if ((u & pmask) == prefix) atomicAdd(&hist[wave][(u >> shift) & 255u], 1u);
+    unsigned zeros = 0;   // elements equal to 0 that match the prefix (all fall in digit 0), counted per wave
+    auto count = [&](unsigned u) {
+      const bool match = (u & pmask) == prefix;
+      const bool z = match && u == 0u;
+      zeros += __popcll(__ballot(z));
+      if (match && !z) atomicAdd(&hist[wave][(u >> shift) & dmask], 1u);
+    };
+    if (in_regs) {
+#pragma unroll
+      for (int i = 0; i < kTopkRegs; ++i) count(v[i]);
+    } else {
+      for (int64_t e0 = 0; e0 < n; e0 += kTopkThreads) {
+        const int64_t e = e0 + tid;
+        count(e < n ? bits[e] : 0xffffffffu);
+      }
     }
+    if (lane == 0 && zeros) atomicAdd(&hist[wave][0], zeros);
     __syncthreads();
     if (tid < 256) {
       unsigned c = 0;
@@ -197,39 +226,50 @@ __global__ __launch_bounds__(kTopkThreads) void topk_emit_kernel(const float* __
     __syncthreads();
     prefix = s_prefix;
     rank = s_rank;
-    pmask |= 255u << shift;
+    pmask |= dmask << shift;
   }
-  const float thr = __uint_as_float(prefix);
+  if (tid == 0) thr_out[row] = __uint_as_float(prefix);
+}
 
-  // emit for every query row of this slice: one wave per row
+// Mask, selection bytes and key lists from the row thresholds: one wave per query row (head, query block). Lists
+// hold the selected key blocks ascending, then the unselected ascending (argSort(!sel) of SparseAttention.swift:177
+// with a stable order).
+__global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict__ probs,
+                                                        const float* __restrict__ thr, int heads, int nq, int nk,
+                                                        int q_slices, float* __restrict__ mask_out,
+                                                        uint8_t* __restrict__ sel, int32_t* __restrict__ kidx,
+                                                        int32_t* __restrict__ kcnt) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);   // h * nq + qi
+  if (row >= heads * nq) return;
+  const int h = row / nq, qi = row - h * nq;
+  const int sq = nq / q_slices;
+  const float th = thr[h * q_slices + qi / sq];
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int i = wave; i < sq; i += kTopkThreads / 64) {
-    const int qi = t * sq + i;
-    const int64_t roff = ((int64_t)h * nq + qi) * nk;
-    const float* prow = probs + roff;
-    int32_t* krow = kidx + roff;
-    int n_sel = 0;
-    for (int j0 = 0; j0 < nk; j0 += 64) {
-      const int j = j0 + lane;
-      const bool s = j < nk && prow[j] > thr;
-      const uint64_t b = __ballot(s);
-      if (s) krow[n_sel + __popcll(b & lt)] = j;
-      if (j < nk) {
-        sel[roff + j] = s ? 1 : 0;
-        if (mask_out) mask_out[roff + j] = s ? 1.f : 0.f;
-      }
-      n_sel += __popcll(b);
+  const int64_t roff = (int64_t)row * nk;
+  const float* prow = probs + roff;
+  int32_t* krow = kidx + roff;
+  int n_sel = 0;
+  for (int j0 = 0; j0 < nk; j0 += 64) {
+    const int j = j0 + lane;
+    const bool s = j < nk && prow[j] > th;
+    const uint64_t b = __ballot(s);
+    if (s) krow[n_sel + __popcll(b & lt)] = j;
+    if (j < nk) {
+      sel[roff + j] = s ? 1 : 0;
+      if (mask_out) mask_out[roff + j] = s ? 1.f : 0.f;
     }
-    int n_un = n_sel;
-    for (int j0 = 0; j0 < nk; j0 += 64) {
-      const int j = j0 + lane;
-      const bool u = j < nk && !(prow[j] > thr);
-      const uint64_t b = __ballot(u);
-      if (u) krow[n_un + __popcll(b & lt)] = j;
-      n_un += __popcll(b);
-    }
-    if (lane == 0) kcnt[(int64_t)h * nq + qi] = n_sel;
+    n_sel += __popcll(b);
   }
+  int n_un = n_sel;
+  for (int j0 = 0; j0 < nk; j0 += 64) {
+    const int j = j0 + lane;
+    const bool u = j < nk && !(prow[j] > th);
+    const uint64_t b = __ballot(u);
+    if (u) krow[n_un + __popcll(b & lt)] = j;
+    n_un += __popcll(b);
+  }
+  if (lane == 0) kcnt[row] = n_sel;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -261,11 +301,14 @@ int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int hea
   return FVSR_OK;
 }
 
-int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, float* mask_out,
-                     uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream) {
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, float* thr,
+                     float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;
-  hipLaunchKernelGGL(topk_emit_kernel, dim3(heads * q_slices), dim3(kTopkThreads), 0, stream, probs, nq, nk,
-                     q_slices, topk, mask_out, sel, kidx, kcnt);
+  hipLaunchKernelGGL(topk_threshold_kernel, dim3(heads * q_slices), dim3(kTopkThreads), 0, stream, probs, nq, nk,
+                     q_slices, topk, thr);
+  FVSR_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(topk_emit_kernel, dim3((heads * nq + 3) / 4), dim3(256), 0, stream, probs, thr, heads, nq, nk,
+                     q_slices, mask_out, sel, kidx, kcnt);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }
