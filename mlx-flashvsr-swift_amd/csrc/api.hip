@@ -4,6 +4,7 @@
 // preconditions, SparseAttention.swift:173; DiT.swift:166,297), the context workspace, the KV-ring bookkeeping
 // (slot head / count per layer, the trim rule of DiT.swift:532-538) and kernel launches on the caller's stream.
 // No entry point synchronises the host with the device.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -26,14 +27,14 @@ int launch_lists_from_mask(const float* mask, int rows, int nk, int32_t* kidx, i
                            hipStream_t stream);
 int launch_sel_from_lists(const int32_t* kidx, const int32_t* kcnt, int rows, int nk_stride, int nk, uint8_t* sel,
                           hipStream_t stream);
-int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, hipStream_t stream);
+int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream);
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
                           const uint8_t* local, float* probs, hipStream_t stream);
 int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, float* thr,
                      float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
                        int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
-                       hipStream_t stream);
+                       float* partial, hipStream_t stream);
 int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,
                      KeyMap map, hipStream_t stream);
 int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int w, int C, bool to_windows,
@@ -46,7 +47,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // workspace carve for one select + attention call
 struct Carve {
-  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, total;
+  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, partial, total;
 };
 static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   Carve c;
@@ -60,6 +61,7 @@ static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   c.order = off; off += align256((size_t)heads * nq * 4);
   c.counter = off; off += 256;
   c.thr = off; off += align256((size_t)heads * nq * 4);   // per (head, query slice) thresholds (nq >= slices)
+  c.partial = off; off += align256((size_t)std::max(nq, nk) * kPoolParts * C * 4);   // pooling runs
   c.total = off;
   return c;
 }
@@ -84,6 +86,7 @@ struct fvsr_kv_ring {
   void* k = nullptr;         // (layers, capacity * s * 128, C)
   void* v = nullptr;
   float* pooled = nullptr;   // (layers, capacity * s, C)
+  float* partial = nullptr;  // (capacity * s * kPoolParts, C): pooled-key runs of one append
   size_t layer_tokens() const { return (size_t)capacity * s * kBlock; }
   char* layer_k(int l) const { return (char*)k + (size_t)l * layer_tokens() * C * esize(dtype); }
   char* layer_v(int l) const { return (char*)v + (size_t)l * layer_tokens() * C * esize(dtype); }
@@ -215,11 +218,12 @@ static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, con
   float* probs = probs_out ? probs_out : (float*)(ws + cv.probs);
   uint8_t* sel = sel_out ? sel_out : (uint8_t*)(ws + cv.sel);
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
-  if ((rc = launch_pool(dtype, qW, lq, C, pq, stream))) return rc;
+  float* partial = (float*)(ws + cv.partial);
+  if ((rc = launch_pool(dtype, qW, lq, C, pq, partial, stream))) return rc;
   const float* pk = pk_src;
   if (!pk_ready) {
     float* pkw = (float*)(ws + cv.pk);
-    if ((rc = launch_pool(dtype, kW, lk, C, pkw, stream))) return rc;
+    if ((rc = launch_pool(dtype, kW, lk, C, pkw, partial, stream))) return rc;
     pk = pkw;
   }
   if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, stream))) return rc;
@@ -374,11 +378,14 @@ int fvsr_kv_ring_create(fvsr_ctx* ctx, int dtype, int layers, int heads, int bh,
     return set_error(FVSR_ERR_UNSUPPORTED, "a ring layer above 2 GiB is not supported (32-bit buffer offsets)");
   }
   const size_t pooled_bytes = (size_t)layers * capacity_slices * r->s * r->C * sizeof(float);
+  const size_t partial_bytes = (size_t)capacity_slices * r->s * kPoolParts * r->C * sizeof(float);
   if (hipSetDevice(ctx->device) != hipSuccess || hipMalloc(&r->k, kv_bytes) != hipSuccess ||
-      hipMalloc(&r->v, kv_bytes) != hipSuccess || hipMalloc((void**)&r->pooled, pooled_bytes) != hipSuccess) {
+      hipMalloc(&r->v, kv_bytes) != hipSuccess || hipMalloc((void**)&r->pooled, pooled_bytes) != hipSuccess ||
+      hipMalloc((void**)&r->partial, partial_bytes) != hipSuccess) {
     if (r->k) (void)hipFree(r->k);
     if (r->v) (void)hipFree(r->v);
     if (r->pooled) (void)hipFree(r->pooled);
+    if (r->partial) (void)hipFree(r->partial);
     delete r;
     return set_error(FVSR_ERR_OUT_OF_MEMORY, "ring allocation of 2 x " + std::to_string(kv_bytes) + " bytes failed");
   }
@@ -392,6 +399,7 @@ int fvsr_kv_ring_destroy(fvsr_kv_ring* r) {
   (void)hipFree(r->k);
   (void)hipFree(r->v);
   (void)hipFree(r->pooled);
+  (void)hipFree(r->partial);
   delete r;
   return FVSR_OK;
 }
@@ -423,7 +431,7 @@ int fvsr_kv_ring_append(fvsr_kv_ring* r, int layer, const void* k_new, const voi
   const int slot0 = (r->head[layer] + r->count[layer]) % r->capacity;
   rc = launch_ring_append(r->dtype, k_new, v_new, n_slices * r->s, r->C, layout == FVSR_LAYOUT_GRID, r->bh, r->bw,
                           slot0, r->capacity, r->layer_k(layer), r->layer_v(layer), r->layer_pooled(layer),
-                          (hipStream_t)stream);
+                          r->partial, (hipStream_t)stream);
   if (rc) return rc;
   r->count[layer] += n_slices;
   return FVSR_OK;

@@ -25,14 +25,17 @@ __device__ __forceinline__ int64_t window_token_to_grid(int b, int t, int nbh, i
 
 // Copies 128-token blocks between layouts (16 bytes per vector). Block b of the source maps to block dst_block(b)
 // of the destination; tokens inside a block may be gathered from grid order (src_grid) or scattered to grid order
-// (dst_grid). When `pooled` is set, also writes the fp32 mean of each source block (the pooled key).
+// (dst_grid). Grid (blocks, kPoolParts): each workgroup moves one run of 32 tokens, so a one-slice append still
+// spreads over every CU. When `partial` is set it also writes the fp32 sum of its run of src (the keys) to
+// partial[(b * kPoolParts + part) * C + c]; pool_finish_kernel turns the runs into the block mean.
 template <typename T>
 __global__ void block_copy_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, bool src_grid,
                                   bool dst_grid, int nbh, int nbw, int dst_slot0, int capacity, int slice_blocks,
-                                  float* __restrict__ pooled, const T* __restrict__ src2, T* __restrict__ dst2) {
+                                  float* __restrict__ partial, const T* __restrict__ src2, T* __restrict__ dst2) {
   constexpr int VN = 16 / sizeof(T);
+  constexpr int kRun = kBlock / kPoolParts;
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
-  const int b = blockIdx.x;
+  const int b = blockIdx.x, part = blockIdx.y;
   // destination block: ring slot (dst_slot0 + b / s) % capacity, block b % s; identity when capacity == 1 and
   // slice_blocks >= the block count
   const int64_t db = (int64_t)((dst_slot0 + b / slice_blocks) % capacity) * slice_blocks + (b % slice_blocks);
@@ -42,23 +45,49 @@ __global__ void block_copy_kernel(const T* __restrict__ src, T* __restrict__ dst
 #pragma unroll
     for (int e = 0; e < VN; ++e) acc[e] = 0.f;
 #pragma unroll 8
-    for (int t = 0; t < kBlock; ++t) {
+    for (int t = part * kRun; t < (part + 1) * kRun; ++t) {
       const int64_t si = src_grid ? window_token_to_grid(b, t, nbh, nbw) : (int64_t)b * kBlock + t;
       const int64_t di = dst_grid ? window_token_to_grid((int)db, t, nbh, nbw) : db * kBlock + t;
       const u4 x = *(const u4*)(src + si * C + cv * VN);
       *(u4*)(dst + di * C + cv * VN) = x;
       if (src2) *(u4*)(dst2 + di * C + cv * VN) = *(const u4*)(src2 + si * C + cv * VN);
-      if (pooled) {
+      if (partial) {
         const T* xv = (const T*)&x;
 #pragma unroll
         for (int e = 0; e < VN; ++e) acc[e] += (float)xv[e];
       }
     }
-    if (pooled) {
+    if (partial) {
+      float* o = partial + ((int64_t)b * kPoolParts + part) * C + cv * VN;
 #pragma unroll
-      for (int e = 0; e < VN; ++e) pooled[db * C + cv * VN + e] = acc[e] / (float)kBlock;
+      for (int e = 0; e < VN; ++e) o[e] = acc[e];
     }
   }
+}
+
+// Block means from the per-run sums: out[dst(b) * C + c] = ((p0 + p1) + (p2 + p3)) / n_b, n_b = the valid tokens
+// of block b (L tokens in all), dst(b) the ring mapping of block_copy_kernel (identity for plain buffers). The fixed
+// order makes the pooled keys of a ring append and of a plain-buffer pool bit-identical.
+__global__ void pool_finish_kernel(const float* __restrict__ partial, int nb, int C, int64_t L, int dst_slot0,
+                                   int capacity, int slice_blocks, float* __restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)nb * C) return;
+  const int b = (int)(e / C), c = (int)(e - (int64_t)b * C);
+  const float* p = partial + (int64_t)b * kPoolParts * C + c;
+  const float sum = (p[0] + p[C]) + (p[2 * C] + p[3 * C]);
+  const int n = (int)min<int64_t>(kBlock, L - (int64_t)b * kBlock);
+  const int64_t db = (int64_t)((dst_slot0 + b / slice_blocks) % capacity) * slice_blocks + (b % slice_blocks);
+  out[db * C + c] = sum / (float)n;
+}
+
+int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
+                       int slice_blocks, float* out, hipStream_t stream) {
+  const int64_t n = (int64_t)nb * C;
+  if (n <= 0) return FVSR_OK;
+  hipLaunchKernelGGL(pool_finish_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, partial, nb, C, L,
+                     dst_slot0, capacity, slice_blocks, out);
+  FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
 }
 
 // Ring -> window order: logical block j of the held window (slot (head + j/s) % capacity) -> block j of dst.
@@ -82,22 +111,24 @@ static int copy_threads(int C, int esize) {
   return std::min(1024, ((nvec + 63) / 64) * 64);
 }
 
+// partial: (n_blocks * kPoolParts, C) fp32 scratch for the pooled-key runs
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
                        int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
-                       hipStream_t stream) {
+                       float* partial, hipStream_t stream) {
   if (n_blocks <= 0) return FVSR_OK;
   const int s = nbh * nbw;
+  const dim3 grid(n_blocks, kPoolParts);
   if (dtype == FVSR_DTYPE_BF16) {
-    hipLaunchKernelGGL(block_copy_kernel<bf16>, dim3(n_blocks), dim3(copy_threads(C, 2)), 0, stream,
-                       (const bf16*)k_new, (bf16*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s,
-                       pooled, (const bf16*)v_new, (bf16*)ring_v);
+    hipLaunchKernelGGL(block_copy_kernel<bf16>, grid, dim3(copy_threads(C, 2)), 0, stream, (const bf16*)k_new,
+                       (bf16*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s, partial,
+                       (const bf16*)v_new, (bf16*)ring_v);
   } else {
-    hipLaunchKernelGGL(block_copy_kernel<float>, dim3(n_blocks), dim3(copy_threads(C, 4)), 0, stream,
-                       (const float*)k_new, (float*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s,
-                       pooled, (const float*)v_new, (float*)ring_v);
+    hipLaunchKernelGGL(block_copy_kernel<float>, grid, dim3(copy_threads(C, 4)), 0, stream, (const float*)k_new,
+                       (float*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s, partial,
+                       (const float*)v_new, (float*)ring_v);
   }
   FVSR_HIP_CHECK(hipGetLastError());
-  return FVSR_OK;
+  return launch_pool_finish(partial, n_blocks, C, (int64_t)n_blocks * kBlock, slot0, capacity, s, pooled, stream);
 }
 
 int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,
@@ -121,11 +152,11 @@ int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int 
   if (n_blocks <= 0) return FVSR_OK;
   const int big = 1 << 30;   // identity destination mapping
   if (dtype == FVSR_DTYPE_BF16)
-    hipLaunchKernelGGL(block_copy_kernel<bf16>, dim3(n_blocks), dim3(copy_threads(C, 2)), 0, stream,
+    hipLaunchKernelGGL(block_copy_kernel<bf16>, dim3(n_blocks, kPoolParts), dim3(copy_threads(C, 2)), 0, stream,
                        (const bf16*)x, (bf16*)out, C, to_windows, !to_windows, nbh, nbw, 0, 1, big,
                        (float*)nullptr, (const bf16*)nullptr, (bf16*)nullptr);
   else
-    hipLaunchKernelGGL(block_copy_kernel<float>, dim3(n_blocks), dim3(copy_threads(C, 4)), 0, stream,
+    hipLaunchKernelGGL(block_copy_kernel<float>, dim3(n_blocks, kPoolParts), dim3(copy_threads(C, 4)), 0, stream,
                        (const float*)x, (float*)out, C, to_windows, !to_windows, nbh, nbw, 0, 1, big,
                        (float*)nullptr, (const float*)nullptr, (float*)nullptr);
   FVSR_HIP_CHECK(hipGetLastError());

@@ -9,7 +9,8 @@
 //   k = min(n - 1, topk).
 //
 // Kernels (all HBM/L2-bound, no MFMA — the score product is 0.1 GFLOP):
-//   pool_kernel          one workgroup per 128-token block: coalesced 16-byte loads, fp32 sums, mean
+//   pool_part_kernel     one workgroup per run of 32 tokens of a block: coalesced 16-byte loads, fp32 sums; the
+//                        means come from pool_finish_kernel (kv_ring.hip) in a fixed order
 //   scores_softmax_kernel one workgroup per (8 query blocks, head): pooled-key rows read once per 8 query rows,
 //                         scores + local mask staged in LDS, one wave per row for max / exp / sum / normalise
 //   topk_threshold_kernel one 1024-thread workgroup per (head, query slice): exact (k+1)-th largest by a 4-pass
@@ -36,14 +37,16 @@ struct Vec16<bf16> {
   typedef bf16x8 type;
 };
 
-// x: (L, C) tokens; out: (nb, C) fp32 means; block b pools rows [b*128, min(L, b*128+128)).
+// x: (L, C) tokens; grid (nb, kPoolParts): run `part` of block b sums rows [b*128 + 32*part, +32) that exist into
+// partial[(b * kPoolParts + part) * C + c] (fp32); pool_finish_kernel forms the block means.
 template <typename T>
-__global__ void pool_kernel(const T* __restrict__ x, int64_t L, int C, float* __restrict__ out) {
+__global__ void pool_part_kernel(const T* __restrict__ x, int64_t L, int C, float* __restrict__ partial) {
   constexpr int VN = Vec16<T>::N;
+  constexpr int kRun = kBlock / kPoolParts;
   typedef typename Vec16<T>::type VT;
-  const int b = blockIdx.x;
-  const int64_t r0 = (int64_t)b * kBlock;
-  const int n = (int)min<int64_t>(kBlock, L - r0);
+  const int b = blockIdx.x, part = blockIdx.y;
+  const int64_t r0 = (int64_t)b * kBlock + part * kRun;
+  const int n = (int)max<int64_t>(0, min<int64_t>(kRun, L - r0));
   const int nvec = C / VN;
   for (int cv = threadIdx.x; cv < nvec; cv += blockDim.x) {
     float acc[VN];
@@ -56,9 +59,9 @@ __global__ void pool_kernel(const T* __restrict__ x, int64_t L, int C, float* __
 #pragma unroll
       for (int e = 0; e < VN; ++e) acc[e] += (float)v[e];
     }
-    float* o = out + (int64_t)b * C + cv * VN;
+    float* o = partial + ((int64_t)b * kPoolParts + part) * C + cv * VN;
 #pragma unroll
-    for (int e = 0; e < VN; ++e) o[e] = acc[e] / (float)n;
+    for (int e = 0; e < VN; ++e) o[e] = acc[e];
   }
 }
 
@@ -275,18 +278,23 @@ __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict_
 // ------------------------------------------------------------------------------------------------------------
 // launch
 // ------------------------------------------------------------------------------------------------------------
-int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, hipStream_t stream) {
+int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
+                       int slice_blocks, float* out, hipStream_t stream);   // kv_ring.hip
+
+// partial: (ceil(L/128) * kPoolParts, C) fp32 scratch
+int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream) {
   const int nb = (int)ceil_div(L, kBlock);
   if (nb <= 0) return FVSR_OK;
   const int vn = dtype == FVSR_DTYPE_BF16 ? 8 : 4;
   const int nvec = C / vn;
   const int threads = std::min(1024, ((nvec + 63) / 64) * 64);
+  const dim3 grid(nb, kPoolParts);
   if (dtype == FVSR_DTYPE_BF16)
-    hipLaunchKernelGGL(pool_kernel<bf16>, dim3(nb), dim3(threads), 0, stream, (const bf16*)x, L, C, out);
+    hipLaunchKernelGGL(pool_part_kernel<bf16>, grid, dim3(threads), 0, stream, (const bf16*)x, L, C, partial);
   else
-    hipLaunchKernelGGL(pool_kernel<float>, dim3(nb), dim3(threads), 0, stream, (const float*)x, L, C, out);
+    hipLaunchKernelGGL(pool_part_kernel<float>, grid, dim3(threads), 0, stream, (const float*)x, L, C, partial);
   FVSR_HIP_CHECK(hipGetLastError());
-  return FVSR_OK;
+  return launch_pool_finish(partial, nb, C, L, 0, 1, 1 << 30, out, stream);
 }
 
 size_t scores_smem_bytes(int nk) { return sizeof(float) * (size_t)kScoreRows * (kHeadDim + nk); }
