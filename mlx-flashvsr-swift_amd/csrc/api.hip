@@ -29,9 +29,10 @@ int launch_sel_from_lists(const int32_t* kidx, const int32_t* kcnt, int rows, in
                           hipStream_t stream);
 int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream);
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
-                          const uint8_t* local, float* probs, hipStream_t stream);
-int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, float* thr,
-                     float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
+                          const uint8_t* local, float* probs, unsigned* hist, int q_slices, hipStream_t stream);
+size_t hist12_bytes(int heads, int q_slices);
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, const unsigned* hist,
+                     float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
                        int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
                        float* partial, hipStream_t stream);
@@ -47,7 +48,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // workspace carve for one select + attention call
 struct Carve {
-  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, partial, total;
+  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, partial, hist, total;
 };
 static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   Carve c;
@@ -62,6 +63,7 @@ static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   c.counter = off; off += 256;
   c.thr = off; off += align256((size_t)heads * nq * 4);   // per (head, query slice) thresholds (nq >= slices)
   c.partial = off; off += align256((size_t)std::max(nq, nk) * kPoolParts * C * 4);   // pooling runs
+  c.hist = off; off += align256(hist12_bytes(heads, (int)nq));   // nq >= query slices
   c.total = off;
   return c;
 }
@@ -226,9 +228,11 @@ static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, con
     if ((rc = launch_pool(dtype, kW, lk, C, pkw, partial, stream))) return rc;
     pk = pkw;
   }
-  if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, stream))) return rc;
-  return launch_topk_emit(probs, heads, (int)nq, nk, q_slices, topk, (float*)(ws + cv.thr), mask_out, sel, kidx,
-                          kcnt, stream);
+  unsigned* hist = (unsigned*)(ws + cv.hist);
+  if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, hist, q_slices, stream)))
+    return rc;
+  return launch_topk_emit(probs, heads, (int)nq, nk, q_slices, topk, hist, (float*)(ws + cv.thr), mask_out, sel,
+                          kidx, kcnt, stream);
 }
 
 int fvsr_lcsa_select(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const void* kW, int64_t lk, int heads,
