@@ -133,6 +133,24 @@ def test_topk_beyond_row_length_keeps_all_above_minimum(dev):
     np.testing.assert_array_equal(mask.cpu().numpy(), ref_mask)
 
 
+@pytest.mark.parametrize("topk", [2_000, 44_000])
+def test_threshold_bin_paths_1920x1152_local3(dev, topk):
+    """1920x1152 geometry with local range 3: ~94 % of each (head, slice) row of 45630 probs are exact zeros. topk
+    2000 puts the threshold among the nonzero probs (the histogram bin is gathered in LDS); topk 44000 puts it on
+    the zeros, a bin far larger than the LDS candidate buffer, so the full-row radix select runs."""
+    wl = synth.WORKLOADS["sparse_1920x1152_bf16"]
+    q, k, _ = synth.make_qkv(wl, seed=1)
+    local = O.local_block_mask(wl.bh, wl.bw, 3)
+    ref_mask, ref_probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads,
+                                                       wl.q_slices, wl.s, local, topk, lk=wl.lk)
+    mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q.to(dev), k.to(dev), wl.heads, wl.q_slices,
+                                                                   wl.s, local, topk)
+    zeros = float((ref_probs == 0).mean())
+    assert zeros > 0.9
+    check_mask(mask, ref_mask, ref_probs, wl.q_slices, topk)
+    check_lists(mask, kidx, kcnt)
+
+
 def test_select_rejects_uneven_slices(dev):
     q = torch.zeros((3 * 128, 128), device=dev)
     k = torch.zeros((4 * 128, 128), device=dev)
