@@ -30,13 +30,19 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 typedef __attribute__((address_space(3))) char lds_char;
 
-// 3-input max without the NaN-quieting canonicalisation the compiler wraps around fmaxf (inputs are MFMA results
-// or -inf, never NaN)
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+
+// O^T += A B on the matrix core with the accumulator in AGPRs. The library is compiled with the MFMA VGPR form
+// (-amdgpu-mfma-vgpr-form) so the score MFMAs, whose results the VALU reads, write VGPRs: an AGPR result would cost
+// one v_accvgpr_read per score, and those (like v_dot2) stall behind a running MFMA. Only this accumulation keeps the
+// AGPR form, written out here. Hazards the compiler does not see through the asm: the B operand (P) is written by
+// the VALU a barrier before it is read; A (V^T) comes from ds_read, whose lgkmcnt wait the compiler inserts;
+// successive accumulations into one block are >= 7 MFMAs apart; acc_drain() runs before the VALU touches the
+// accumulators again.
+__device__ __forceinline__ void mfma_acc(f32x16& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
+// >= 19 wait states: an 8-pass MFMA result may be read or overwritten by the VALU afterwards
+__device__ __forceinline__ void acc_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 
 // Lazy online-softmax rescale. The running reference max m_run (log2 domain, per query row) is raised only when a
 // tile's row max exceeds it by more than 8, i.e. a factor 2^8: exponentials then stay <= 256 (no overflow in fp32 or
@@ -56,6 +62,15 @@ __device__ __forceinline__ float rescale_if_grown(float mxc, float& m_run, float
     m_run = m_new;
   }
   return m_run == -INFINITY ? 0.f : m_run;
+}
+
+// f(integral_constant<I>) for I = B .. E-1, unrolled at compile time
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -102,12 +117,13 @@ __device__ __forceinline__ int swz_v(int r) { return (r << 1) & 15; }
 // 16 bytes per lane from a buffer straight into LDS at lds_base + OFF + 16 * lane. Issued as inline assembly so the
 // compiler does not order every later LDS read behind it: the kernel orders the copies itself (vmcnt + barrier).
 // M0 is written without a clobber declaration (the compiler reserves it); nothing else in these kernels uses M0. It
-// is loaded with s_mov_b32 from an address computed outside the asm (an s_add_u32 into M0 fed the copy a wrong
-// address on gfx950).
+// is loaded with s_mov_b32 from an address computed outside the asm. GFX9 requires one wait state between an SALU
+// write of M0 and an LDS DMA that reads it; the compiler inserts it for its own code but not inside an asm
+// statement, so the s_nop is written out.
 template <int OFF>
 __device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_base, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_base + OFF), "v"(voff),
-               "s"(rsrc), "s"(soff));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_base + OFF),
+               "v"(voff), "s"(rsrc), "s"(soff));
 }
 
 __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
@@ -291,31 +307,15 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         const bf16x8 vv = __builtin_bit_cast(bf16x8, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int q = 0; q < 2; ++q)
-          acc[q][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p[q][u], acc[q][dt], 0, 0, 0);
+          mfma_acc(acc[q][dt], vv, p[q][u]);
       }
   };
-  const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
-  // P = exp2(S^T) packed to bf16 (u-th 16-key step = accumulator entries 8u .. 8u+7); partial row sum over the same
-  // bf16-rounded values
-  auto expo = [&](const f32x16& s, bf16x8 (&p)[2]) -> float {
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[u][e] = (bf16)__builtin_amdgcn_exp2f(s[8 * u + e]);
-    float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 0, 1), ones, s0, false);
-      s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 2, 3), ones, s1, false);
-      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 4, 5), ones, s0, false);
-      s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(p[u], p[u], 6, 7), ones, s1, false);
-    }
-    return s0 + s1;
-  };
   auto row_max = [&](const f32x16& s) -> float {
-    float mx = vmax3(s[0], s[1], s[2]);
+    // plain fmaxf, not v_max3 in inline asm: s comes straight from an MFMA (VGPR form), and the compiler inserts the
+    // MFMA -> VALU wait states only for instructions it can see
+    float mx = fmaxf(s[0], s[1]);
 #pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = vmax3(mx, s[r], s[r + 1]);
+    for (int r = 2; r < 15; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
     return pair_max(fmaxf(mx, s[15]));
   };
   // all of this wave's copies but the last `keep` steps' have landed, and every wave is past its LDS reads
@@ -407,17 +407,18 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 #pragma unroll
         for (int q = 0; q < 2; ++q) m_row[q] = fmaxf(m_row[q], row_max(s_cur[q]));
       } else {
-        // Nine rounds, each fenced so the order below is the issue order. Round 0: the reference / mask MFMA of
-        // QK(T+1) for both query groups and 8 exponentials of S(T), work that needs no LDS operand. Round r = 1..8:
-        // MFMA r of QK(T+1) for both groups, the PV(T-1) MFMA pair r-1 and (r <= 6) 4 more exponentials. Every
-        // round also requests the LDS operands of the round two ahead and (r < 8) one of the 8 buffer->LDS copies of
-        // this step, so no burst of memory instructions stalls the matrix core. The two dependent QK chains see 3
-        // other MFMAs between their links.
+        // 34 micro-rounds, one MFMA each, fenced so the order below is the issue order. A wave issues in order and
+        // an MFMA occupies the matrix core for 32 cycles: every MFMA is followed by a slice of the other work, which
+        // issues while it runs (MFMAs grouped back to back would leave that work unoverlapped). MFMA order: the
+        // reference / mask MFMA of QK(T+1) for both query groups, then for c = 0..7 QK chunk c (group 0, group 1)
+        // and PV pair c (group 0, group 1); the dependent QK links are 3 MFMAs apart. Slices: exponential I of S(T)
+        // in micro-round I (pairs packed to bf16 and summed on odd I); the LDS operands of chunk / pair j requested
+        // at least 4 micro-rounds before use; one of the 8 buffer->LDS copies of the step every 4 micro-rounds.
         lds_char* const vbase = lds + kVRing + ((SUB + 3) & 3) * kTileBytes;
         lds_char* const kbase = lds + ((SUB + 1) & 3) * kTileBytes;
         i16x4 va[8], vb[8];
         bf16x8 kk[8];
-        // operands of round j + 1: V^T pair j (PV) and K chunk j (QK)
+        // operands of QK chunk j and PV pair j: K chunk j and V^T pair j
         auto read_ops = [&](int j) {
           lds_char* const pa = vbase + v_off[j & 3] + 16 * (j >> 2) * kRowBytes;
           va[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
@@ -431,60 +432,45 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         };
         const bf16x8 ax = aext(valid_next);
         float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
-        // exponentials of S(T) entries 4h .. 4h+3 (pairs packed to bf16) of 16-key step u, group q; chunk c = 0..7
-        auto expo4 = [&](int c) {
-          const int q = c >> 2, u = (c >> 1) & 1, h = c & 1;
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            bf16x2 pr;
-            pr[0] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e]);
-            pr[1] = (bf16)__builtin_amdgcn_exp2f(s_cur[q][8 * u + 4 * h + e + 1]);
-            p_cur[q][u][4 * h + e] = pr[0];
-            p_cur[q][u][4 * h + e + 1] = pr[1];
-            sum[q][e >> 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, sum[q][e >> 1], false);
-          }
-        };
-        auto round = [&](auto r_c) {
-          constexpr int r = decltype(r_c)::value;
-          if constexpr (r == 0) {
+        float x_even = 0.f;
+        auto micro = [&](auto i_c) {
+          constexpr int I = decltype(i_c)::value;
+          if constexpr (I == 0) {
             read_ops(0);
             read_ops(1);
-          } else if constexpr (r + 1 < 8) {
-            read_ops(r + 1);
+          } else if constexpr ((I & 3) == 3 && (I + 5) / 4 < 8) {
+            read_ops((I + 5) / 4);
           }
-#pragma unroll
-          for (int q = 0; q < 2; ++q)
-            s_nxt[q] = r == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0)
-                              : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[r == 0 ? 0 : r - 1], qop[q][r == 0 ? 0 : r - 1],
-                                                                        s_nxt[q], 0, 0, 0);
-          if constexpr (r >= 1) {
-            // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword
-            // duplicated)
-            constexpr int j = r - 1;
-            const bf16x8 vv =
-                __builtin_bit_cast(bf16x8, __builtin_shufflevector(va[j], vb[j], 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-              acc[q][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vv, p_prev[q][j >> 2], acc[q][j & 3], 0, 0, 0);
+          if constexpr (I < 2) {
+            s_nxt[I] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[I], f32x16{}, 0, 0, 0);
+          } else {
+            constexpr int c = (I - 2) / 4, w = (I - 2) % 4;
+            if constexpr (w < 2) {
+              s_nxt[w] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[c], qop[w][c], s_nxt[w], 0, 0, 0);
+            } else {
+              // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword
+              // duplicated)
+              const bf16x8 vv =
+                  __builtin_bit_cast(bf16x8, __builtin_shufflevector(va[c], vb[c], 0, 1, 2, 3, 4, 5, 6, 7));
+              mfma_acc(acc[w - 2][c & 3], vv, p_prev[w - 2][c >> 2]);
+            }
           }
-          if constexpr (r == 0) {
-            expo4(0);
-            expo4(1);
-          } else if constexpr (r <= 6) {
-            expo4(r + 1);
+          if constexpr (I < 32) {
+            // S(T) entry idx of group q; fp32 sums (v_dot2 would wait for the matrix core)
+            constexpr int q = I >> 4, idx = I & 15;
+            const float x = __builtin_amdgcn_exp2f(s_cur[q][idx]);
+            if constexpr ((I & 1) == 0) {
+              x_even = x;
+            } else {
+              p_cur[q][idx >> 3][(idx & 7) - 1] = (bf16)x_even;
+              p_cur[q][idx >> 3][idx & 7] = (bf16)x;
+              sum[q][(idx >> 1) & 1] += x_even + x;
+            }
           }
-          if constexpr (r < 8) dma(r_c);
+          if constexpr ((I & 3) == 1 && I / 4 < 8) dma(std::integral_constant<int, I / 4>{});
           __builtin_amdgcn_sched_barrier(0);
         };
-        round(C0{});
-        round(C1{});
-        round(C2{});
-        round(C3{});
-        round(std::integral_constant<int, 4>{});
-        round(std::integral_constant<int, 5>{});
-        round(std::integral_constant<int, 6>{});
-        round(std::integral_constant<int, 7>{});
-        round(std::integral_constant<int, 8>{});
+        static_for<0, 34>(micro);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           const float part = sum[q][0] + sum[q][1];
@@ -507,7 +493,10 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
       o0 = o1; o1 = o2; o2 = o3;
       n0 = n1; n1 = n2; n2 = n3;
     }
-    if (MODE != 1) pv(C3{}, pB);   // PV of the last tile (4 * nblocks - 1, slot 3)
+    if (MODE != 1) {
+      pv(C3{}, pB);   // PV of the last tile (4 * nblocks - 1, slot 3)
+      acc_drain();
+    }
     // drain the zero-fill copies requested past the end before LDS is reused
     FVSR_WAIT_VM_LGKM0(0);
     __builtin_amdgcn_s_barrier();
