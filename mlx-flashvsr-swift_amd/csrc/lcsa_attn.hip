@@ -11,6 +11,7 @@
 // online-softmax rescale. Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of (head, query
 // block) items: adjacent query blocks select overlapping key blocks, so K/V tiles hit in L2.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.hpp"
@@ -102,7 +103,6 @@ constexpr int kRowBytes = kHeadDim * 2;                // one head of one token,
 constexpr int kTileBytes = kTileKeys * kRowBytes;      // 8 KB
 constexpr int kSlots = 4;                              // per ring: slot of tile T = T mod 4 = its quarter of the block
 constexpr int kVRing = kSlots * kTileBytes;            // byte offset of the V ring
-constexpr int kDmaPerStep = 8;                         // per wave and step: 4 K + 4 V loads of 1 KB
 constexpr float kMaskedScore = -1.2676506e30f;         // -2^100: exp2 of a masked key is exactly 0
 
 // 16-byte chunk swizzles. K: the 8 (or 16) lanes one ds_read_b128 cycle serves read 8 (16) consecutive rows of one
@@ -138,14 +138,22 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 }  // namespace
 
-template <bool DENSE>
-__global__ __attribute__((amdgpu_flat_work_group_size(128, 128), amdgpu_waves_per_eu(1, 1)))
+// LDS operand requests of chunk / pair j >= 2 (j = 0, 1: micro-round 0), in micro-rounds of a step with QG query
+// groups per wave: 7 (QG 2) or 4 (QG 1) micro-rounds before the QK MFMA that uses them
+template <int QG>
+constexpr int attn_read_at(int j) { return QG + 2 * QG * j - (QG == 2 ? 7 : 4); }
+
+template <bool DENSE, int QG>
+__global__ __attribute__((amdgpu_flat_work_group_size(256 / QG, 256 / QG), amdgpu_waves_per_eu(3 - QG, 3 - QG)))
 void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_t* __restrict__ kcnt,
                       const uint8_t* __restrict__ sel, const bf16* __restrict__ Q, bf16* __restrict__ O,
                       const int32_t* __restrict__ order, int32_t* __restrict__ counter) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kVRing];
   __shared__ int item_s;
 
+  // QG 32-query groups per wave: 4 / QG waves of 32 * QG queries; every wave copies 8 * QG rows of each tile
+  constexpr int kWaves = 4 / QG, kThreads = 64 * kWaves, kQW = 32 * QG, kWaveRows = 8 * QG;
+  constexpr int kDmaK = 2 * QG, kDmaStep = 4 * QG;   // per wave: copies of one K (V) tile, of one step
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
@@ -164,7 +172,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   const int cnt = kcnt[row_id];
 
   if (cnt <= 0) {   // empty query block -> zeros (SparseAttention.swift:47-53; DiT.swift:300-304)
-    for (int e = tid; e < kBlock * 16; e += 128) {
+    for (int e = tid; e < kBlock * 16; e += kThreads) {
       const int64_t row = (int64_t)qb * kBlock + (e >> 4);
       if (row < a.lq) *(u32x4*)(O + row * a.ld + hc + (e & 15) * 8) = u32x4{0, 0, 0, 0};
     }
@@ -174,12 +182,12 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   const uint8_t* __restrict__ srow = DENSE ? sel + (int64_t)row_id * a.nk : nullptr;
   const int nblocks = DENSE ? a.nk : min(cnt, a.nk_stride);
 
-  // Q as the B operand of S^T = K Q^T, prescaled by c: group q holds queries qb*128 + 64*wave + 32*q + l32,
+  // Q as the B operand of S^T = K Q^T, prescaled by c: group q holds queries qb*128 + kQW*wave + 32*q + l32,
   // lane (query, k-half g) dims 16t + 8g .. +7
-  bf16x8 qop[2][8];
+  bf16x8 qop[QG][8];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int64_t qrow = (int64_t)qb * kBlock + wave * 64 + q * 32 + l32;
+  for (int q = 0; q < QG; ++q) {
+    const int64_t qrow = (int64_t)qb * kBlock + wave * kQW + q * 32 + l32;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       bf16x8 x = bf16x8{};
@@ -197,16 +205,16 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   const uint32_t row_bytes = (uint32_t)a.ld * 2;
   const uint32_t range = (uint32_t)(a.kv_rows * row_bytes);
   const u32x4 krs = buffer_rsrc(a.k, range), vrs = buffer_rsrc(a.v, range);
-  // a DMA load writes 1 KB of LDS (lane i -> bytes 16i..16i+15) = 4 rows; wave w fills rows 16w .. 16w+15
-  int voff_k[4], voff_v[4];
+  // a DMA load writes 1 KB of LDS (lane i -> bytes 16i..16i+15) = 4 rows; wave w fills rows kWaveRows * w ..
+  int voff_k[kDmaK], voff_v[kDmaK];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int r = wave * 16 + 4 * p + (lane >> 4), pos = lane & 15;
+  for (int p = 0; p < kDmaK; ++p) {
+    const int r = wave * kWaveRows + 4 * p + (lane >> 4), pos = lane & 15;
     voff_k[p] = r * (int)row_bytes + hc * 2 + ((pos ^ swz_k(r)) << 4);
     voff_v[p] = r * (int)row_bytes + hc * 2 + ((pos ^ swz_v(r)) << 4);
   }
   const uint32_t smem_lds = lds_addr(smem);
-  const uint32_t dma_base = smem_lds + wave * 16 * kRowBytes;
+  const uint32_t dma_base = smem_lds + wave * kWaveRows * kRowBytes;
   // buffer byte offset of block j's first row (j outside [0, nk): past the buffer -> zeros)
   auto block_soff = [&](int j) -> int {
     return (unsigned)j < (unsigned)a.nk ? (int)(a.map.row(j) * row_bytes) : (int)range;
@@ -215,19 +223,19 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   // K / V of quarter SUB of the block at soff into ring slot SLOT
   auto issue_k = [&](auto slot_c, int soff) {
     constexpr int SLOT = decltype(slot_c)::value;
-    dma16<SLOT * kTileBytes + 0 * 4 * kRowBytes>(krs, dma_base, voff_k[0], soff);
-    dma16<SLOT * kTileBytes + 1 * 4 * kRowBytes>(krs, dma_base, voff_k[1], soff);
-    dma16<SLOT * kTileBytes + 2 * 4 * kRowBytes>(krs, dma_base, voff_k[2], soff);
-    dma16<SLOT * kTileBytes + 3 * 4 * kRowBytes>(krs, dma_base, voff_k[3], soff);
+    static_for<0, kDmaK>([&](auto p_c) {
+      constexpr int P = decltype(p_c)::value;
+      dma16<SLOT * kTileBytes + P * 4 * kRowBytes>(krs, dma_base, voff_k[P], soff);
+    });
   };
   auto issue_v = [&](auto slot_c, int soff) {
     constexpr int SLOT = decltype(slot_c)::value;
-    dma16<kVRing + SLOT * kTileBytes + 0 * 4 * kRowBytes>(vrs, dma_base, voff_v[0], soff);
-    dma16<kVRing + SLOT * kTileBytes + 1 * 4 * kRowBytes>(vrs, dma_base, voff_v[1], soff);
-    dma16<kVRing + SLOT * kTileBytes + 2 * 4 * kRowBytes>(vrs, dma_base, voff_v[2], soff);
-    dma16<kVRing + SLOT * kTileBytes + 3 * 4 * kRowBytes>(vrs, dma_base, voff_v[3], soff);
+    static_for<0, kDmaK>([&](auto p_c) {
+      constexpr int P = decltype(p_c)::value;
+      dma16<kVRing + SLOT * kTileBytes + P * 4 * kRowBytes>(vrs, dma_base, voff_v[P], soff);
+    });
   };
-  // one of the 4 copies (rows 4P .. 4P+3 of this wave's half) of K / V into ring slot SLOT
+  // one of the kDmaK copies (rows 4P .. 4P+3 of this wave's share) of K / V into ring slot SLOT
   auto dma_k = [&](auto slot_c, auto p_c, int soff) {
     constexpr int SLOT = decltype(slot_c)::value, P = decltype(p_c)::value;
     dma16<SLOT * kTileBytes + P * 4 * kRowBytes>(krs, dma_base, voff_k[P], soff);
@@ -258,10 +266,10 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   for (int dt = 0; dt < 4; ++dt)
     v_off[dt] = vr * kRowBytes + (((4 * dt + 2 * (G & 1) + ((mm & 3) >> 1)) ^ swz_v(vr)) << 4) + (mm & 1) * 8;
 
-  f32x16 acc[2][4];
-  float l_run[2], m_row[2], part_max[2];
+  f32x16 acc[QG][4];
+  float l_run[QG], m_row[QG], part_max[QG];
   // the extra MFMA step: A lane (key l32, g = 0) holds k-slots {1, masked}, B lane (query, g = 0) {-m, -2^100}
-  bf16x8 bext[2];
+  bf16x8 bext[QG];
   auto set_ref = [&](int q, float m) {
     bf16x8 b = bf16x8{};
     if (g == 0) {
@@ -280,21 +288,21 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   };
   lds_char* const lds = (lds_char*)(uintptr_t)smem_lds;
   // S^T = K Q^T - m (keys that do not take part: - 2^100) for both groups, K from ring slot SLOT
-  auto qk = [&](auto slot_c, int valid, f32x16 (&s)[2]) {
+  auto qk = [&](auto slot_c, int valid, f32x16 (&s)[QG]) {
     constexpr int SLOT = decltype(slot_c)::value;
     bf16x8 kk[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) kk[t] = *(const lds_bf16x8*)(lds + SLOT * kTileBytes + k_off[t]);
     const bf16x8 ax = aext(valid);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0);
+    for (int q = 0; q < QG; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[t], qop[q][t], s[q], 0, 0, 0);
+      for (int q = 0; q < QG; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[t], qop[q][t], s[q], 0, 0, 0);
   };
   // O^T += V^T P^T, V from ring slot SLOT
-  auto pv = [&](auto slot_c, const bf16x8 (&p)[2][2]) {
+  auto pv = [&](auto slot_c, const bf16x8 (&p)[QG][2]) {
     constexpr int SLOT = decltype(slot_c)::value;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -306,7 +314,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword duplicated)
         const bf16x8 vv = __builtin_bit_cast(bf16x8, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < QG; ++q)
           mfma_acc(acc[q][dt], vv, p[q][u]);
       }
   };
@@ -320,8 +328,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   };
   // all of this wave's copies but the last `keep` steps' have landed, and every wave is past its LDS reads
   auto sync_steps = [&](int keep) {
-    if (keep >= 2) FVSR_WAIT_VM_LGKM0(2 * kDmaPerStep);
-    else if (keep == 1) FVSR_WAIT_VM_LGKM0(kDmaPerStep);
+    if (keep >= 2) FVSR_WAIT_VM_LGKM0(2 * kDmaStep);
+    else if (keep == 1) FVSR_WAIT_VM_LGKM0(kDmaStep);
     else FVSR_WAIT_VM_LGKM0(0);
     __builtin_amdgcn_s_barrier();
   };
@@ -339,7 +347,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   auto run = [&](auto mode_c) {
     constexpr int MODE = decltype(mode_c)::value;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < QG; ++q) {
       l_run[q] = 0.f;
       part_max[q] = 0.f;
 #pragma unroll
@@ -347,8 +355,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
       set_ref(q, MODE == 2 ? m_row[q] : 0.f);
       if (MODE == 1) m_row[q] = kMaskedScore;
     }
-    f32x16 sA[2], sB[2];
-    bf16x8 pA[2][2], pB[2][2];
+    f32x16 sA[QG], sB[QG];
+    bf16x8 pA[QG][2], pB[QG][2];
     // per walked block: first-row buffer offset and keys taking part, read two blocks ahead of use
     int o0 = walk_soff(0), o1 = walk_soff(1), o2 = walk_soff(2);
     int n0 = walk_keys(0), n1 = walk_keys(1), n2 = walk_keys(2);
@@ -363,7 +371,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
                                              : 0,
          sA);
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < QG; ++q) {
         const float mx = row_max(sA[q]);
         set_ref(q, (float)(bf16)(mx > kNoKey ? mx : 0.f));
       }
@@ -381,22 +389,22 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
       // reference = the exact row max of tile 0; the tile is then recomputed with it inside the accumulator, the
       // same arithmetic as every later tile (and as the dense walk)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < QG; ++q) {
         const float mx = row_max(sA[q]);
         set_ref(q, (float)(bf16)(mx > kNoKey ? mx : 0.f));
       }
       qk(C0{}, sub_valid(n0, 0), sA);
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < QG; ++q)
 #pragma unroll
       for (int u = 0; u < 2; ++u) pB[q][u] = bf16x8{};
     sync_steps(2);   // K(1), V(-1) landed
 
     // step with tile T in ring slot SUB: K(T+4) -> slot SUB, V(T+2) -> slot SUB+2, QK(T+1) <- K slot SUB+1,
     // PV(T-1) <- V slot SUB+3 (all mod 4)
-    auto step = [&](auto sub_c, int valid_next, int soff_k, int soff_v, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2],
-                    bf16x8 (&p_prev)[2][2], bf16x8 (&p_cur)[2][2]) {
+    auto step = [&](auto sub_c, int valid_next, int soff_k, int soff_v, f32x16 (&s_cur)[QG], f32x16 (&s_nxt)[QG],
+                    bf16x8 (&p_prev)[QG][2], bf16x8 (&p_cur)[QG][2]) {
       constexpr int SUB = decltype(sub_c)::value;
       using KS = std::integral_constant<int, SUB>;
       using VS = std::integral_constant<int, (SUB + 2) & 3>;
@@ -405,15 +413,15 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         issue_v(VS{}, soff_v);
         qk(std::integral_constant<int, (SUB + 1) & 3>{}, valid_next, s_nxt);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) m_row[q] = fmaxf(m_row[q], row_max(s_cur[q]));
+        for (int q = 0; q < QG; ++q) m_row[q] = fmaxf(m_row[q], row_max(s_cur[q]));
       } else {
-        // 34 micro-rounds, one MFMA each, fenced so the order below is the issue order. A wave issues in order and
-        // an MFMA occupies the matrix core for 32 cycles: every MFMA is followed by a slice of the other work, which
-        // issues while it runs (MFMAs grouped back to back would leave that work unoverlapped). MFMA order: the
-        // reference / mask MFMA of QK(T+1) for both query groups, then for c = 0..7 QK chunk c (group 0, group 1)
-        // and PV pair c (group 0, group 1); the dependent QK links are 3 MFMAs apart. Slices: exponential I of S(T)
-        // in micro-round I (pairs packed to bf16 and summed on odd I); the LDS operands of chunk / pair j requested
-        // at least 4 micro-rounds before use; one of the 8 buffer->LDS copies of the step every 4 micro-rounds.
+        // 17 * QG micro-rounds, one MFMA each, fenced so the order below is the issue order. A wave issues in order
+        // and an MFMA occupies the matrix core for 32 cycles: every MFMA is followed by a slice of the other work,
+        // which issues while it runs (MFMAs grouped back to back would leave that work unoverlapped). MFMA order: the
+        // reference / mask MFMA of QK(T+1) for each query group, then for c = 0..7 QK chunk c (each group) and PV
+        // pair c (each group). Slices: exponential I of S(T) in micro-round I (pairs packed to bf16 and summed on odd
+        // I); the LDS operands of chunk / pair j requested at least 4 micro-rounds before use (attn_read_at); one of
+        // the step's buffer->LDS copies every 4 micro-rounds.
         lds_char* const vbase = lds + kVRing + ((SUB + 3) & 3) * kTileBytes;
         lds_char* const kbase = lds + ((SUB + 1) & 3) * kTileBytes;
         i16x4 va[8], vb[8];
@@ -427,35 +435,39 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         };
         auto dma = [&](auto r_c) {
           constexpr int R = decltype(r_c)::value;
-          if constexpr (R < 4) dma_k(KS{}, std::integral_constant<int, R>{}, soff_k);
-          else dma_v(VS{}, std::integral_constant<int, R - 4>{}, soff_v);
+          if constexpr (R < kDmaK) dma_k(KS{}, std::integral_constant<int, R>{}, soff_k);
+          else dma_v(VS{}, std::integral_constant<int, R - kDmaK>{}, soff_v);
         };
         const bf16x8 ax = aext(valid_next);
-        float sum[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+        float sum[QG][2];
+#pragma unroll
+        for (int q = 0; q < QG; ++q) sum[q][0] = sum[q][1] = 0.f;
         float x_even = 0.f;
         auto micro = [&](auto i_c) {
           constexpr int I = decltype(i_c)::value;
           if constexpr (I == 0) {
             read_ops(0);
             read_ops(1);
-          } else if constexpr ((I & 3) == 3 && (I + 5) / 4 < 8) {
-            read_ops((I + 5) / 4);
           }
-          if constexpr (I < 2) {
+          static_for<2, 8>([&](auto j_c) {
+            constexpr int J = decltype(j_c)::value;
+            if constexpr (attn_read_at<QG>(J) == I) read_ops(J);
+          });
+          if constexpr (I < QG) {
             s_nxt[I] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[I], f32x16{}, 0, 0, 0);
           } else {
-            constexpr int c = (I - 2) / 4, w = (I - 2) % 4;
-            if constexpr (w < 2) {
+            constexpr int c = (I - QG) / (2 * QG), w = (I - QG) % (2 * QG);
+            if constexpr (w < QG) {
               s_nxt[w] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[c], qop[w][c], s_nxt[w], 0, 0, 0);
             } else {
               // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword
               // duplicated)
               const bf16x8 vv =
                   __builtin_bit_cast(bf16x8, __builtin_shufflevector(va[c], vb[c], 0, 1, 2, 3, 4, 5, 6, 7));
-              mfma_acc(acc[w - 2][c & 3], vv, p_prev[w - 2][c >> 2]);
+              mfma_acc(acc[w - QG][c & 3], vv, p_prev[w - QG][c >> 2]);
             }
           }
-          if constexpr (I < 32) {
+          if constexpr (I < 16 * QG) {
             // S(T) entry idx of group q; fp32 sums (v_dot2 would wait for the matrix core)
             constexpr int q = I >> 4, idx = I & 15;
             const float x = __builtin_amdgcn_exp2f(s_cur[q][idx]);
@@ -467,12 +479,12 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
               sum[q][(idx >> 1) & 1] += x_even + x;
             }
           }
-          if constexpr ((I & 3) == 1 && I / 4 < 8) dma(std::integral_constant<int, I / 4>{});
+          if constexpr ((I & 3) == 1 && I / 4 < kDmaStep) dma(std::integral_constant<int, I / 4>{});
           __builtin_amdgcn_sched_barrier(0);
         };
-        static_for<0, 34>(micro);
+        static_for<0, 17 * QG>(micro);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < QG; ++q) {
           const float part = sum[q][0] + sum[q][1];
           l_run[q] += part;
           if (MODE == 0) part_max[q] = fmaxf(part_max[q], part);
@@ -508,7 +520,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   {
     bool bad = false;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < QG; ++q) {
       const float pm = pair_max(part_max[q]);
       bad |= !(pm <= 4294967296.f) || pm < 2.3283064e-10f;
     }
@@ -522,17 +534,16 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     if (redo) {
       run(std::integral_constant<int, 1>{});
 #pragma unroll
-      for (int q = 0; q < 2; ++q) m_row[q] = (float)(bf16)(m_row[q] > kNoKey ? m_row[q] : 0.f);
+      for (int q = 0; q < QG; ++q) m_row[q] = (float)(bf16)(m_row[q] > kNoKey ? m_row[q] : 0.f);
       run(std::integral_constant<int, 2>{});
     }
   }
 
-  const float l0 = pair_sum(l_run[0]), l1 = pair_sum(l_run[1]);
-  const float inv0 = l0 > 0.f ? 1.f / l0 : 0.f, inv1 = l1 > 0.f ? 1.f / l1 : 0.f;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int64_t qrow = (int64_t)qb * kBlock + wave * 64 + q * 32 + l32;
-    const float inv = q ? inv1 : inv0;
+  for (int q = 0; q < QG; ++q) {
+    const float l = pair_sum(l_run[q]);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int64_t qrow = (int64_t)qb * kBlock + wave * kQW + q * 32 + l32;
     if (qrow < a.lq) {
       bf16* orow = O + qrow * a.ld + hc;
 #pragma unroll
@@ -826,6 +837,16 @@ static int device_cus() {
   return cus[dev];
 }
 
+// query groups per wave of the bf16 walk: 1 (4 waves of 32 queries, two waves per SIMD) unless FVSR_ATTN_QG=2
+// (2 waves of 64 queries, one wave per SIMD)
+static int attn_query_groups() {
+  static const int qg = [] {
+    const char* e = getenv("FVSR_ATTN_QG");
+    return (e && e[0] == '2') ? 2 : 1;
+  }();
+  return qg;
+}
+
 int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t stream) {
   const int nwg = a.heads * a.nq;
   if (nwg <= 0) return FVSR_OK;
@@ -834,14 +855,23 @@ int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t strea
     if (!a.order || !a.counter) return set_error(FVSR_ERR_INVALID_ARG, "attention: no workspace for the row order");
     hipLaunchKernelGGL(attn_order_kernel, dim3(1), dim3(1024), 0, stream, a.kcnt, nwg, a.nk_stride, dense ? 1 : 0,
                        a.order, a.counter);
-    // two workgroups (64 KB of LDS, one wave per SIMD each) are resident per CU
+    // two workgroups (64 KB of LDS each) are resident per CU
     const dim3 pgrid(std::min(nwg, 2 * device_cus()));
-    if (dense)
-      hipLaunchKernelGGL(attn_bf16_kernel<true>, pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
-                         (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
-    else
-      hipLaunchKernelGGL(attn_bf16_kernel<false>, pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
-                         (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
+    if (attn_query_groups() == 2) {
+      if (dense)
+        hipLaunchKernelGGL((attn_bf16_kernel<true, 2>), pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                           (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
+      else
+        hipLaunchKernelGGL((attn_bf16_kernel<false, 2>), pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                           (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
+    } else {
+      if (dense)
+        hipLaunchKernelGGL((attn_bf16_kernel<true, 1>), pgrid, dim3(256), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                           (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
+      else
+        hipLaunchKernelGGL((attn_bf16_kernel<false, 1>), pgrid, dim3(256), 0, stream, a, a.kidx, a.kcnt, a.sel,
+                           (const bf16*)a.q, (bf16*)a.o, (const int32_t*)a.order, a.counter);
+    }
   } else {
     if (dense) hipLaunchKernelGGL(attn_f32_kernel<true>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(attn_f32_kernel<false>, grid, block, 0, stream, a);
