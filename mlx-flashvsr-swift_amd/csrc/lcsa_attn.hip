@@ -4,12 +4,12 @@
 // blockMaskedAttention (DiT.swift:279-313): per head, o = softmax(q k^T / sqrt(128)) v over the listed key blocks,
 // fp32 online softmax, a query block with no listed key block writes zeros.
 //
-// bf16 (the production lane): one workgroup = one (head, 128-query block) = 2 wave64s x 64 queries, one wave per
-// SIMD; K/V tiles of 32 keys reach LDS by direct buffer->LDS copies into 4-slot rings; S^T = K Q^T and O^T += V^T P^T
-// on v_mfma_f32_32x32x16_bf16 so each lane owns one query row; the softmax keeps a fixed reference per row (see the
-// kernel's comment). fp32 (the parity lane): 4 wave64s x 32 queries on v_mfma_f32_32x32x2_f32 with a lazy
-// online-softmax rescale. Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of (head, query
-// block) items: adjacent query blocks select overlapping key blocks, so K/V tiles hit in L2.
+// bf16 (the production lane): a persistent walk over rows (head, 128-query block); a workgroup = 4 wave64s x 32
+// queries, two waves per SIMD; K/V tiles of 32 keys reach LDS by direct buffer->LDS copies into 4-slot rings;
+// S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16_bf16 so each lane owns one query row; the softmax keeps a fixed
+// reference per row (see the kernel's comment). fp32 (the parity lane): 4 wave64s x 32 queries on
+// v_mfma_f32_32x32x2_f32 with a lazy online-softmax rescale; workgroup ids are remapped so each XCD (own L2) walks a
+// contiguous run of (head, query block) items.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
@@ -77,14 +77,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 // ------------------------------------------------------------------------------------------------------------
 // bf16
 // ------------------------------------------------------------------------------------------------------------
-// One workgroup = one (head, 128-query block) = 2 wave64s x 64 queries, one wave per SIMD (up to 512 registers),
-// two workgroups per CU. Each wave holds its 64 queries as two 32-query groups; every K or V operand it reads from
-// LDS feeds two MFMAs (one per group), so LDS supplies one byte per 64 FLOP.
+// One workgroup = one (head, 128-query block) at a time, two workgroups per CU. QG = 1 (the default): 4 wave64s x 32
+// queries, two waves per SIMD (at most 256 registers each), so one wave's LDS, memory and VALU stalls are covered by
+// the other's MFMAs. QG = 2: 2 wave64s x 64 queries held as two 32-query groups, one wave per SIMD; every K or V
+// operand read from LDS then feeds two MFMAs.
 //
 // Keys stream in tiles of 32 (a quarter of a 128-key block). K and V tiles land in two LDS rings of kSlots slots by
 // buffer_load ... lds (16 B per lane, no VGPR staging); a tile's rows are 256 B (one head) with the 16-byte chunks
 // XOR-swizzled by row so the ds_read_b128 (K) and ds_read_b64_tr_b16 (V^T) operand reads are bank-conflict free.
-// K of tile T+5 and V of tile T+3 are requested while tile T is processed: every copy has 4 tile steps to land.
+// While tile T is processed (step T), K of tile T+4 and V of tile T+2 are requested; they are waited for two steps
+// later, before the step that reads them.
 //
 // Softmax with a fixed reference per query row: Q is prescaled by log2(e)/sqrt(128) and one extra rank-2 MFMA step
 // per tile adds -m (the row's reference, the exact max of its first tile) and -2^100 for keys of the tile that do
