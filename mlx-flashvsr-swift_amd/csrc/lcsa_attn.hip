@@ -270,23 +270,27 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 
   f32x16 acc[QG][4];
   float l_run[QG], m_row[QG], part_max[QG];
-  // the extra MFMA step: A lane (key l32, g = 0) holds k-slots {1, masked}, B lane (query, g = 0) {-m, -2^100}
-  bf16x8 bext[QG];
+  // the extra MFMA step, a v_mfma_f32_32x32x8_bf16 (k = 8, half the cost of a k = 16 step): A lane (key l32, g = 0)
+  // holds k-slots {1, masked}, B lane (query, g = 0) {-m, -2^100}, all other k-slots 0
+  i16x4 bext[QG];
   auto set_ref = [&](int q, float m) {
-    bf16x8 b = bf16x8{};
+    bf16x4 b = bf16x4{};
     if (g == 0) {
       b[0] = (bf16)(-m);
       b[1] = (bf16)kMaskedScore;
     }
-    bext[q] = b;
+    bext[q] = __builtin_bit_cast(i16x4, b);
   };
-  auto aext = [&](int valid) -> bf16x8 {
-    bf16x8 x = bf16x8{};
+  auto aext = [&](int valid) -> i16x4 {
+    bf16x4 x = bf16x4{};
     if (g == 0) {
       x[0] = (bf16)1.0f;
       x[1] = l32 >= valid ? (bf16)1.0f : (bf16)0.0f;
     }
-    return x;
+    return __builtin_bit_cast(i16x4, x);
+  };
+  auto mfma_ext = [&](const i16x4& ax, const i16x4& bx) -> f32x16 {
+    return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ax, bx, f32x16{}, 0, 0, 0);
   };
   lds_char* const lds = (lds_char*)(uintptr_t)smem_lds;
   // S^T = K Q^T - m (keys that do not take part: - 2^100) for both groups, K from ring slot SLOT
@@ -295,9 +299,9 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     bf16x8 kk[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) kk[t] = *(const lds_bf16x8*)(lds + SLOT * kTileBytes + k_off[t]);
-    const bf16x8 ax = aext(valid);
+    const i16x4 ax = aext(valid);
 #pragma unroll
-    for (int q = 0; q < QG; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[q], f32x16{}, 0, 0, 0);
+    for (int q = 0; q < QG; ++q) s[q] = mfma_ext(ax, bext[q]);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -440,7 +444,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           if constexpr (R < kDmaK) dma_k(KS{}, std::integral_constant<int, R>{}, soff_k);
           else dma_v(VS{}, std::integral_constant<int, R - kDmaK>{}, soff_v);
         };
-        const bf16x8 ax = aext(valid_next);
+        const i16x4 ax = aext(valid_next);
         float sum[QG][2];
 #pragma unroll
         for (int q = 0; q < QG; ++q) sum[q][0] = sum[q][1] = 0.f;
@@ -456,7 +460,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
             if constexpr (attn_read_at<QG>(J) == I) read_ops(J);
           });
           if constexpr (I < QG) {
-            s_nxt[I] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ax, bext[I], f32x16{}, 0, 0, 0);
+            s_nxt[I] = mfma_ext(ax, bext[I]);
           } else {
             constexpr int c = (I - QG) / (2 * QG), w = (I - QG) % (2 * QG);
             if constexpr (w < QG) {
