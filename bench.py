@@ -45,6 +45,8 @@ def parse_args():
                          "6-latent-frame first chunk and 4 chunks of 2 latent frames; append + select + attention + "
                          "evict per layer call; prints its own JSON line")
     ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--epilogue", action="store_true",
+                    help="time the fused QKV epilogue into the KV ring on one 1920x1152 streaming chunk (HBM-bound)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain copy of known size (the window-partition kernel over 16x72x120 bf16 "
                          "tokens of 1536 channels: 424.7 MB read + 424.7 MB written per launch), the reference "
@@ -217,6 +219,56 @@ def stream_bench(args):
     print(json.dumps(line), flush=True)
 
 
+def epilogue_bench(args):
+    """The projection epilogue of one streaming chunk at 1920x1152 (2 latent frames, 17280 tokens, 12 x 128 heads,
+    bf16): WanRMSNorm of q and k, 3-D RoPE, window partition, K/V appended to the ring with pooled keys
+    (DiT.swift:34-47,100-118,496-511), one kernel plus the pooled-key finish. HBM-bound: reports GB/s of the
+    algorithmic bytes (q, k, v read once; Q, K, V written once; the pooled-key runs written and read once)."""
+    import torch
+
+    import fvsr_lcsa
+
+    dev = torch.device("cuda:0")
+    H, bh, bw = 12, 9, 15
+    s, C = bh * bw, H * 128
+    f, h, w = 2, 8 * bh, 8 * bw
+    L = f * h * w
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    q, k, v = (torch.randn((L, C), generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
+    wq = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
+    wk = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
+    ring = fvsr_lcsa.KVRing(1, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    qo = torch.empty_like(q)
+
+    def once():
+        ring.append_qkv(0, q, k, v, 1, 6, wq, wk, q_out=qo)
+        ring.evict(0)
+        if ring.slices(0) >= 3:
+            ring.reset()
+
+    for _ in range(max(3, args.warmup)):
+        once()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(10, args.steps)
+    e0.record()
+    for _ in range(n):
+        once()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    nbytes = 6 * L * C * 2 + 2 * (L // 128) * 4 * C * 4 + (L // 128) * C * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "fused QKV epilogue into the KV ring, one 1920x1152 streaming chunk",
+        "value": round(gbs, 1), "unit": "GB/s (algorithmic bytes)", "ms_per_call": round(ms, 4),
+        "higher_is_better": True, "n_gpus": 1, "dtype": "bf16", "data": "synthetic (seeded N(0,1))",
+        "config": {"workload": "epilogue_1920x1152_bf16", "tokens": L, "channels": C, "heads": H},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(gbs / 8000.0, 4), "traffic": None},
+        "algorithmic_bytes": nbytes}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -234,6 +286,9 @@ def main():
         return
     if args.stream:
         stream_bench(args)
+        return
+    if args.epilogue:
+        epilogue_bench(args)
         return
     dev = torch.device("cuda:0")
     wl = synth.WORKLOADS[args.workload]

@@ -150,6 +150,28 @@ int fvsr_lcsa_layer(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const void* qW
                     const void* v_new, int n_new_slices, int layout, int q_slices, const uint8_t* local_dev,
                     int topk, int mode, void* o, float* mask_out, float* probs_out, void* stream);
 
+/* ---- (f1) fused QKV epilogue: RMSNorm + 3-D RoPE + window partition ------------------------------------------ */
+/* RoPE tables of `RopeTables(headDim: 128, theta:)` (DiT.swift:52-97), HOST function: fills `out` (at least
+ * fvsr_rope_tables_size() floats) with cos_t, sin_t (1024 x 22), cos_h, sin_h (1024 x 21), cos_w, sin_w (1024 x 21),
+ * row p = position p, computed in double and stored fp32 like the reference. Upload them once per device. */
+size_t fvsr_rope_tables_size(void);
+int fvsr_rope_tables(double theta, float* out, size_t n_floats);
+
+/* The projections' epilogue of `blockForward` (DiT.swift:496-506): q' = ropeApply(normQ(q)), k' = ropeApply(normK(k))
+ * with WanRMSNorm over the full width (DiT.swift:34-47: fp32 normalise with eps, cast, times weight) and ropeApply
+ * at temporal positions t0 .. t0+f-1 (DiT.swift:100-107), then windowPartition (DiT.swift:111-118) of q', k' and v.
+ * q, k, v: (f*h*w, heads*128) natural (f, h, w) token order, `dtype`; norm weights: (heads*128) `dtype`;
+ * rope_tables: device copy of fvsr_rope_tables. Outputs q_out, k_out, v_out: (f*h*w, heads*128) window order. */
+int fvsr_qkv_epilogue(fvsr_ctx* ctx, int dtype, const void* q, const void* k, const void* v, int f, int h, int w,
+                      int heads, int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                      const float* rope_tables, void* q_out, void* k_out, void* v_out, void* stream);
+/* The same epilogue straight into the KV ring: appends the chunk's k' and v (f = 2*n_slices, h = 8*bh, w = 8*bw,
+ * natural token order) to `layer` like fvsr_kv_ring_append (pooled keys included) and writes q' in window order to
+ * q_out. Replaces the projection epilogue and the cache concat of blockForward (DiT.swift:496-511). */
+int fvsr_kv_ring_append_qkv(fvsr_kv_ring* ring, int layer, const void* q, const void* k, const void* v, int n_slices,
+                            int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                            const float* rope_tables, void* q_out, void* stream);
+
 /* ---- (a1) window layout ------------------------------------------------------------------------------------ */
 /* Replace `windowPartition` / `windowReverse` (DiT.swift:113-126): (f*h*w, C) natural <-> window order. */
 int fvsr_window_partition(int dtype, const void* x, void* out, int f, int h, int w, int channels, void* stream);

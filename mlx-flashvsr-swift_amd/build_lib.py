@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libfvsr_lcsa.so")
 PROBE = os.path.join(LIB_DIR, "fvsr_probe_attn")
 
-SOURCES = ["api.hip", "lcsa_attn.hip", "lcsa_select.hip", "kv_ring.hip"]
+SOURCES = ["api.hip", "lcsa_attn.hip", "lcsa_select.hip", "kv_ring.hip", "qkv_epilogue.hip"]
 # Packed-FP32 VALU forms are disabled: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32 from float code.
 # MFMA builtins get the VGPR form (results in VGPRs, where the VALU reads them without v_accvgpr_read); the attention
 # kernels write the one AGPR-accumulating MFMA as inline assembly.

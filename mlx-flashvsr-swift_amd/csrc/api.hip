@@ -33,6 +33,14 @@ int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int hea
 size_t hist12_bytes(int heads, int q_slices);
 int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, const unsigned* hist,
                      float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
+int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int C, int t0,
+                        const void* wq, const void* wk, float eps, const float* rope, void* q_out, void* k_out,
+                        void* v_out, int dst_slot0, int capacity, int slice_blocks, hipStream_t stream);
+int launch_pool_parts(int dtype, const void* x, int64_t L, int C, float* partial, hipStream_t stream);
+int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
+                       int slice_blocks, float* out, hipStream_t stream);
+int rope_table_floats();
+void rope_tables_host(double theta, float* out);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
                        int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
                        float* partial, hipStream_t stream);
@@ -356,6 +364,49 @@ int fvsr_window_reverse(int dtype, const void* x, void* out, int f, int h, int w
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// fused QKV epilogue (RMSNorm + RoPE + window partition)
+// ---------------------------------------------------------------------------------------------------------------
+size_t fvsr_rope_tables_size(void) { return (size_t)rope_table_floats(); }
+
+int fvsr_rope_tables(double theta, float* out, size_t n_floats) {
+  FVSR_REQUIRE(out != nullptr, FVSR_ERR_INVALID_ARG, "out is NULL");
+  FVSR_REQUIRE(n_floats >= (size_t)rope_table_floats(), FVSR_ERR_INVALID_ARG,
+               "out holds fewer than fvsr_rope_tables_size() floats");
+  FVSR_REQUIRE(theta > 1.0, FVSR_ERR_INVALID_ARG, "theta must be > 1");
+  rope_tables_host(theta, out);
+  return FVSR_OK;
+}
+
+static int check_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int heads,
+                          int t0, const void* wq, const void* wk, float eps, const float* rope) {
+  FVSR_REQUIRE(valid_dtype(dtype), FVSR_ERR_INVALID_ARG, "dtype must be FVSR_DTYPE_F32 or FVSR_DTYPE_BF16");
+  FVSR_REQUIRE(q && k && v && wq && wk && rope, FVSR_ERR_INVALID_ARG,
+               "q, k, v, the norm weights and the RoPE tables must be non-NULL");
+  FVSR_REQUIRE(f > 0 && h > 0 && w > 0 && f % 2 == 0 && h % 8 == 0 && w % 8 == 0, FVSR_ERR_INVALID_ARG,
+               "window (2, 8, 8) must tile (f, h, w)");
+  int rc = check_heads(heads);
+  if (rc) return rc;
+  FVSR_REQUIRE(heads * 128 * esize(dtype) / 16 <= 1024, FVSR_ERR_UNSUPPORTED,
+               "the epilogue handles at most 1024 16-byte vectors per token");
+  FVSR_REQUIRE(t0 >= 0 && t0 + f <= 1024 && h <= 1024 && w <= 1024, FVSR_ERR_INVALID_ARG,
+               "token positions must lie inside the 1024-row RoPE tables");
+  FVSR_REQUIRE(eps >= 0.f, FVSR_ERR_INVALID_ARG, "eps must be >= 0");
+  return FVSR_OK;
+}
+
+int fvsr_qkv_epilogue(fvsr_ctx* ctx, int dtype, const void* q, const void* k, const void* v, int f, int h, int w,
+                      int heads, int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                      const float* rope_tables, void* q_out, void* k_out, void* v_out, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_epilogue(dtype, q, k, v, f, h, w, heads, t0, norm_q_weight, norm_k_weight, eps, rope_tables);
+  if (rc) return rc;
+  FVSR_REQUIRE(q_out && k_out && v_out, FVSR_ERR_INVALID_ARG, "q_out, k_out and v_out must be non-NULL");
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_qkv_epilogue(dtype, q, k, v, f, h, w, heads * 128, t0, norm_q_weight, norm_k_weight, eps,
+                             rope_tables, q_out, k_out, v_out, 0, 1, 1 << 30, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // KV ring
 // ---------------------------------------------------------------------------------------------------------------
 int fvsr_kv_ring_create(fvsr_ctx* ctx, int dtype, int layers, int heads, int bh, int bw, int capacity_slices,
@@ -436,6 +487,45 @@ int fvsr_kv_ring_append(fvsr_kv_ring* r, int layer, const void* k_new, const voi
   rc = launch_ring_append(r->dtype, k_new, v_new, n_slices * r->s, r->C, layout == FVSR_LAYOUT_GRID, r->bh, r->bw,
                           slot0, r->capacity, r->layer_k(layer), r->layer_v(layer), r->layer_pooled(layer),
                           r->partial, (hipStream_t)stream);
+  if (rc) return rc;
+  r->count[layer] += n_slices;
+  return FVSR_OK;
+}
+
+int fvsr_kv_ring_append_qkv(fvsr_kv_ring* r, int layer, const void* q, const void* k, const void* v, int n_slices,
+                            int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                            const float* rope_tables, void* q_out, void* stream) {
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(n_slices > 0, FVSR_ERR_INVALID_ARG, "n_slices must be > 0");
+  rc = check_epilogue(r->dtype, q, k, v, 2 * n_slices, 8 * r->bh, 8 * r->bw, r->heads, t0, norm_q_weight,
+                      norm_k_weight, eps, rope_tables);
+  if (rc) return rc;
+  FVSR_REQUIRE(q_out != nullptr, FVSR_ERR_INVALID_ARG, "q_out is NULL");
+  FVSR_REQUIRE(r->count[layer] + n_slices <= r->capacity, FVSR_ERR_CAPACITY,
+               "append of " + std::to_string(n_slices) + " slices exceeds the ring capacity of " +
+                   std::to_string(r->capacity) + " (held " + std::to_string(r->count[layer]) + ")");
+  FVSR_HIP_CHECK(hipSetDevice(r->ctx->device));
+  const int slot0 = (r->head[layer] + r->count[layer]) % r->capacity;
+  const int nb = n_slices * r->s;
+  rc = launch_qkv_epilogue(r->dtype, q, k, v, 2 * n_slices, 8 * r->bh, 8 * r->bw, r->C, t0, norm_q_weight,
+                           norm_k_weight, eps, rope_tables, q_out, r->layer_k(layer), r->layer_v(layer), slot0,
+                           r->capacity, r->s, (hipStream_t)stream);
+  if (rc) return rc;
+  // pooled keys of the new slots, as for plain buffers: block sums over the slots up to the end of the ring, then
+  // the wrapped remainder from slot 0
+  const int first = std::min(n_slices, r->capacity - slot0);
+  const size_t slot_bytes = (size_t)r->s * kBlock * r->C * esize(r->dtype);
+  rc = launch_pool_parts(r->dtype, r->layer_k(layer) + slot0 * slot_bytes, (int64_t)first * r->s * kBlock, r->C,
+                         r->partial, (hipStream_t)stream);
+  if (rc) return rc;
+  if (first < n_slices) {
+    rc = launch_pool_parts(r->dtype, r->layer_k(layer), (int64_t)(n_slices - first) * r->s * kBlock, r->C,
+                           r->partial + (size_t)first * r->s * kPoolParts * r->C, (hipStream_t)stream);
+    if (rc) return rc;
+  }
+  rc = launch_pool_finish(r->partial, nb, r->C, (int64_t)nb * kBlock, slot0, r->capacity, r->s,
+                          r->layer_pooled(layer), (hipStream_t)stream);
   if (rc) return rc;
   r->count[layer] += n_slices;
   return FVSR_OK;

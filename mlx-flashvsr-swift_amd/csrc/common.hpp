@@ -80,4 +80,15 @@ struct AttnArgs {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// token t (0..127) of window b -> natural (f, h, w) token index, windows ordered (nf, nh, nw), tokens (wf, wh, ww)
+// (windowPartition, DiT.swift:113-118)
+__device__ __forceinline__ int64_t window_token_to_grid(int b, int t, int nbh, int nbw) {
+  const int per_slice = nbh * nbw;
+  const int nf = b / per_slice, rem = b % per_slice;
+  const int nh = rem / nbw, nw = rem % nbw;
+  const int wf = t >> 6, wh = (t >> 3) & 7, ww = t & 7;
+  const int64_t H = 8 * nbh, W = 8 * nbw;
+  return ((int64_t)(2 * nf + wf) * H + 8 * nh + wh) * W + 8 * nw + ww;
+}
+
 }  // namespace fvsr

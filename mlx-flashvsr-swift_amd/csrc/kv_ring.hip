@@ -13,16 +13,6 @@
 
 namespace fvsr {
 
-// token t (0..127) of window b -> natural (f, h, w) token index, windows ordered (nf, nh, nw), tokens (wf, wh, ww)
-__device__ __forceinline__ int64_t window_token_to_grid(int b, int t, int nbh, int nbw) {
-  const int per_slice = nbh * nbw;
-  const int nf = b / per_slice, rem = b % per_slice;
-  const int nh = rem / nbw, nw = rem % nbw;
-  const int wf = t >> 6, wh = (t >> 3) & 7, ww = t & 7;
-  const int64_t H = 8 * nbh, W = 8 * nbw;
-  return ((int64_t)(2 * nf + wf) * H + 8 * nh + wh) * W + 8 * nw + ww;
-}
-
 // Copies 128-token blocks between layouts (16 bytes per vector). Block b of the source maps to block dst_block(b)
 // of the destination; tokens inside a block may be gathered from grid order (src_grid) or scattered to grid order
 // (dst_grid). Grid (blocks, kPoolParts): each workgroup moves one run of 32 tokens, so a one-slice append still

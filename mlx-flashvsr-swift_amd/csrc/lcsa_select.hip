@@ -438,8 +438,8 @@ __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict_
 int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
                        int slice_blocks, float* out, hipStream_t stream);   // kv_ring.hip
 
-// partial: (ceil(L/128) * kPoolParts, C) fp32 scratch
-int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream) {
+// the per-run block sums of x (L tokens): partial[(b * kPoolParts + part) * C + c], (ceil(L/128) * kPoolParts, C)
+int launch_pool_parts(int dtype, const void* x, int64_t L, int C, float* partial, hipStream_t stream) {
   const int nb = (int)ceil_div(L, kBlock);
   if (nb <= 0) return FVSR_OK;
   const int vn = dtype == FVSR_DTYPE_BF16 ? 8 : 4;
@@ -451,6 +451,15 @@ int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* p
   else
     hipLaunchKernelGGL(pool_part_kernel<float>, grid, dim3(threads), 0, stream, (const float*)x, L, C, partial);
   FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+// block means of x: partial (ceil(L/128) * kPoolParts, C) fp32 scratch
+int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream) {
+  const int nb = (int)ceil_div(L, kBlock);
+  if (nb <= 0) return FVSR_OK;
+  const int rc = launch_pool_parts(dtype, x, L, C, partial, stream);
+  if (rc) return rc;
   return launch_pool_finish(partial, nb, C, L, 0, 1, 1 << 30, out, stream);
 }
 

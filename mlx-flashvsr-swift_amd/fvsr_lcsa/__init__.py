@@ -9,6 +9,8 @@ Names mirror the reference's call surface (xocialize/mlx-flashvsr-swift):
   FlashVSRAttentionOps        FlashVSRAttentionOps.dense / .kernel             SparseAttention.swift:190-202
   KVRing                      the window K/V cache of blockForward             DiT.swift:507-511,532-538
   window_partition / reverse  windowPartition / windowReverse                  DiT.swift:113-126
+  rope_tables                 RopeTables(headDim: 128)                          DiT.swift:52-97
+  qkv_epilogue                normQ/normK + ropeApply + windowPartition          DiT.swift:34-47,100-118,496-506
 Token tensors are (L, H*128) or (1, L, H*128), window order, float32 or bfloat16, on a HIP device, contiguous.
 Every call runs the HIP kernels of libfvsr_lcsa.so; there is no CPU fallback.
 """
@@ -26,6 +28,7 @@ from ._abi import (ATTN_AUTO, ATTN_DENSE, ATTN_KERNEL, DTYPE_BF16, DTYPE_F32, LA
 __all__ = ["FVSRError", "Context", "local_block_mask", "draft_block_mask_and_probs", "draft_block_mask",
            "kernel_block_attention", "block_masked_attention", "block_sparse_attention", "FlashVSRAttentionOps",
            "KVRing", "window_partition", "window_reverse", "attention_mode_auto", "workspace_size",
+           "rope_tables", "rope_tables_device", "qkv_epilogue",
            "ATTN_AUTO", "ATTN_DENSE", "ATTN_KERNEL", "LAYOUT_GRID", "LAYOUT_WINDOWS", "lib"]
 
 HEAD_DIM = 128
@@ -231,6 +234,48 @@ def window_reverse(x, f: int, h: int, w: int, stream=None):
 
 
 # ------------------------------------------------------------------------------------------------------------------
+# fused QKV epilogue
+# ------------------------------------------------------------------------------------------------------------------
+def rope_tables(theta: float = 10000.0) -> np.ndarray:
+    """RoPE tables of RopeTables(headDim: 128, theta:) (DiT.swift:52-97), host fp32: cos_t, sin_t (1024 x 22),
+    cos_h, sin_h, cos_w, sin_w (1024 x 21 each), concatenated. Computed by the library (fvsr_rope_tables)."""
+    n = int(lib.fvsr_rope_tables_size())
+    out = np.empty(n, dtype=np.float32)
+    call("fvsr_rope_tables", float(theta), out.ctypes.data_as(C.c_void_p), n)
+    return out
+
+
+_rope_dev: dict[tuple, torch.Tensor] = {}
+
+
+def rope_tables_device(device, theta: float = 10000.0) -> torch.Tensor:
+    """Device copy of rope_tables(theta), uploaded once per (device, theta)."""
+    dev = torch.device(device)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), float(theta))
+    t = _rope_dev.get(key)
+    if t is None:
+        t = torch.from_numpy(rope_tables(theta)).to(f"cuda:{key[0]}")
+        _rope_dev[key] = t
+    return t
+
+
+def qkv_epilogue(q, k, v, f: int, h: int, w: int, heads: int, t0: int, norm_q_weight, norm_k_weight,
+                 eps: float = 1e-6, theta: float = 10000.0, stream=None):
+    """(q', k', v) in window order from the projections q, k, v ((f*h*w, heads*128), natural token order):
+    normQ/normK (WanRMSNorm over the full width) + ropeApply at temporal positions t0.. + windowPartition
+    (DiT.swift:34-47,100-118,496-506). Returns (q_out, k_out, v_out)."""
+    q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+    ctx = Context.get(q2.device)
+    wq = norm_q_weight.to(q2.dtype).contiguous()
+    wk = norm_k_weight.to(q2.dtype).contiguous()
+    tab = rope_tables_device(q2.device, theta)
+    qo, ko, vo = torch.empty_like(q2), torch.empty_like(k2), torch.empty_like(v2)
+    call("fvsr_qkv_epilogue", ctx.handle, _dtype_code(q2), _ptr(q2), _ptr(k2), _ptr(v2), f, h, w, heads, t0,
+         _ptr(wq), _ptr(wk), float(eps), _ptr(tab), _ptr(qo), _ptr(ko), _ptr(vo), _stream(stream))
+    return qo, ko, vo
+
+
+# ------------------------------------------------------------------------------------------------------------------
 # KV ring
 # ------------------------------------------------------------------------------------------------------------------
 class KVRing:
@@ -265,6 +310,19 @@ class KVRing:
     def append(self, layer: int, k_new, v_new, n_slices: int, layout: int = LAYOUT_WINDOWS, stream=None):
         k2, v2 = _tokens(k_new, "k_new"), _tokens(v_new, "v_new")
         call("fvsr_kv_ring_append", self.handle, layer, _ptr(k2), _ptr(v2), n_slices, layout, _stream(stream))
+
+    def append_qkv(self, layer: int, q, k, v, n_slices: int, t0: int, norm_q_weight, norm_k_weight,
+                   eps: float = 1e-6, theta: float = 10000.0, stream=None, q_out=None):
+        """The projection epilogue straight into the ring (DiT.swift:496-511): appends k' = rope(normK(k)) and v of
+        the chunk (natural token order, f = 2 * n_slices) and returns q' = rope(normQ(q)) in window order."""
+        q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+        wq = norm_q_weight.to(q2.dtype).contiguous()
+        wk = norm_k_weight.to(q2.dtype).contiguous()
+        tab = rope_tables_device(q2.device, theta)
+        qo = torch.empty_like(q2) if q_out is None else _tokens(q_out, "q_out")
+        call("fvsr_kv_ring_append_qkv", self.handle, layer, _ptr(q2), _ptr(k2), _ptr(v2), n_slices, t0, _ptr(wq),
+             _ptr(wk), float(eps), _ptr(tab), _ptr(qo), _stream(stream))
+        return qo
 
     def evict(self, layer: int):
         call("fvsr_kv_ring_evict", self.handle, layer)

@@ -42,6 +42,11 @@ SIGNATURES = {
     "fvsr_lcsa_select_ring": (_i, [_vp, _vp, _i, _vp, _i64, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "fvsr_lcsa_attention_ring": (_i, [_vp, _vp, _i, _vp, _i64, _vp, _vp, _i, _i, _vp, _vp]),
     "fvsr_lcsa_layer": (_i, [_vp, _vp, _i, _vp, _i64, _vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _vp]),
+    "fvsr_rope_tables_size": (_sz, []),
+    "fvsr_rope_tables": (_i, [C.c_double, _vp, _sz]),
+    "fvsr_qkv_epilogue": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp,
+                               _vp]),
+    "fvsr_kv_ring_append_qkv": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _vp]),
     "fvsr_window_partition": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "fvsr_window_reverse": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
 }

@@ -15,6 +15,10 @@ It restates, in numpy, what the reference (xocialize/mlx-flashvsr-swift) compute
   step_topk / default_topk_ratio       Sources/FlashVSRMLX/DiT.swift:478-485; Pipeline.swift:68
   compare (rel metric)                 Sources/Smoke/Gates.swift:19-29
   mask_flip_report (near-tie rule)     Sources/Smoke/Gates.swift:239-277
+  rope_tables                          Sources/FlashVSRMLX/DiT.swift:52-78
+  wan_rms_norm                         Sources/FlashVSRMLX/DiT.swift:34-47
+  rope_apply                           Sources/FlashVSRMLX/DiT.swift:100-107
+  qkv_epilogue                         Sources/FlashVSRMLX/DiT.swift:496-506 (norm -> rope -> window partition)
 
 Ragged extension (not in the reference, which only ever sees whole 128-token windows and whole temporal slices):
 a token count that is not a multiple of 128 ends in a partial block. Attention slices the expanded token mask to
@@ -57,6 +61,77 @@ def window_reverse(x: np.ndarray, b: int, f: int, h: int, w: int) -> np.ndarray:
     c = x.shape[-1]
     y = x.reshape(b, f // 2, h // 8, w // 8, 2, 8, 8, c).transpose(0, 1, 4, 2, 5, 3, 6, 7)
     return np.ascontiguousarray(y).reshape(b, f * h * w, c)
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# projection epilogue: WanRMSNorm, RoPE, window partition
+# ----------------------------------------------------------------------------------------------------------------
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bfloat16 (round to nearest, ties to even) and return them as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def rope_tables(head_dim: int = HEAD_DIM, end: int = 1024, theta: float = 10000.0) -> list:
+    """`RopeTables.init` (DiT.swift:58-78): per axis (t, h, w) with sub-dims (d - 2(d//3), d//3, d//3), pair j has
+    frequency theta^(-2j/dim) over its OWN sub-dimension; row p = (cos, sin)(p * freq) computed in float64, stored
+    float32. Returns [(cos_t, sin_t), (cos_h, sin_h), (cos_w, sin_w)], each (end, pairs)."""
+    out = []
+    for dim in (head_dim - 2 * (head_dim // 3), head_dim // 3, head_dim // 3):
+        n = dim // 2
+        freq = 1.0 / np.power(float(theta), 2.0 * np.arange(n, dtype=np.float64) / dim)
+        ang = np.arange(end, dtype=np.float64)[:, None] * freq[None, :]
+        out.append((np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)))
+    return out
+
+
+def rope_tables_flat(theta: float = 10000.0) -> np.ndarray:
+    """The tables packed as the C ABI's fvsr_rope_tables lays them out: cos_t, sin_t, cos_h, sin_h, cos_w, sin_w."""
+    return np.concatenate([a.reshape(-1) for pair in rope_tables(theta=theta) for a in pair])
+
+
+def wan_rms_norm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6, bf16: bool = True) -> np.ndarray:
+    """`WanRMSNorm` (DiT.swift:42-46): fp32 x * rsqrt(mean(x^2, last axis) + eps), cast to the input dtype, times
+    the weight (a product rounded to the input dtype). bf16=True models bfloat16 tensors (values exact in bf16)."""
+    xf = x.astype(np.float32)
+    ms = (xf * xf).mean(axis=-1, keepdims=True, dtype=np.float32)
+    n = xf * (np.float32(1.0) / np.sqrt(ms + np.float32(eps), dtype=np.float32))
+    if bf16:
+        return to_bf16(to_bf16(n) * weight.astype(np.float32))
+    return n * weight.astype(np.float32)
+
+
+def rope_apply(x: np.ndarray, heads: int, cos: np.ndarray, sin: np.ndarray, bf16: bool = True) -> np.ndarray:
+    """`ropeApply` (DiT.swift:101-107): view each head as 64 (re = even, im = odd) pairs, multiply by e^{i theta}
+    in fp32 (each product and sum rounded once), cast back. x (L, heads*128); cos, sin (L, 64) fp32."""
+    L, c = x.shape
+    xf = x.astype(np.float32).reshape(L, heads, c // heads // 2, 2)
+    re, im = xf[..., 0], xf[..., 1]
+    cs, sn = cos[:, None, :].astype(np.float32), sin[:, None, :].astype(np.float32)
+    out = np.stack([re * cs - im * sn, re * sn + im * cs], axis=-1).reshape(L, c)
+    return to_bf16(out) if bf16 else out
+
+
+def rope_grid(f: int, h: int, w: int, t0: int, theta: float = 10000.0):
+    """`RopeTables.grid` (DiT.swift:81-97): (cos, sin) of shape (f*h*w, 64) for an (f, h, w) token grid whose
+    temporal positions start at t0."""
+    (ct, st), (ch, sh), (cw, sw) = rope_tables(theta=theta)
+    T, Y, X = np.meshgrid(np.arange(t0, t0 + f), np.arange(h), np.arange(w), indexing="ij")
+    T, Y, X = T.reshape(-1), Y.reshape(-1), X.reshape(-1)
+    return (np.concatenate([ct[T], ch[Y], cw[X]], axis=1), np.concatenate([st[T], sh[Y], sw[X]], axis=1))
+
+
+def qkv_epilogue(q: np.ndarray, k: np.ndarray, v: np.ndarray, f: int, h: int, w: int, heads: int, t0: int,
+                 wq: np.ndarray, wk: np.ndarray, eps: float = 1e-6, bf16: bool = True):
+    """The projection epilogue of blockForward (DiT.swift:498-506): q' = ropeApply(normQ(q)), k' =
+    ropeApply(normK(k)), then windowPartition of q', k', v. q, k, v (f*h*w, C) natural token order; returns the three
+    as (f*h*w, C) window-ordered float32 arrays (bfloat16 values when bf16)."""
+    cos, sin = rope_grid(f, h, w, t0)
+    qn = rope_apply(wan_rms_norm(q, wq, eps, bf16), heads, cos, sin, bf16)
+    kn = rope_apply(wan_rms_norm(k, wk, eps, bf16), heads, cos, sin, bf16)
+    c = q.shape[-1]
+    return tuple(window_partition(x[None].astype(np.float32), f, h, w).reshape(-1, c) for x in (qn, kn, v))
 
 
 # ----------------------------------------------------------------------------------------------------------------

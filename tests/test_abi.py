@@ -96,3 +96,20 @@ def test_python_binding_raises_fvsr_error():
     with pytest.raises(fvsr_lcsa.FVSRError) as ei:
         _abi.call("fvsr_local_block_mask", -1, 4, 3, None)
     assert ei.value.status == _abi.ERR_INVALID_ARG
+
+
+def test_rope_tables_host_matches_oracle():
+    """fvsr_rope_tables (host, no device work) against the oracle's float64 -> float32 tables: equal up to one
+    float32 ulp (the two libm's float64 cos/sin may differ in the last bit before the float32 rounding)."""
+    got = fvsr_lcsa.rope_tables()
+    ref = O.rope_tables_flat()
+    assert got.shape == ref.shape
+    d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    assert (d <= np.spacing(np.abs(ref)).astype(np.float64) + 1e-45).all()
+    assert (got == ref).mean() > 0.999
+
+
+def test_rope_tables_rejects_short_buffer():
+    out = np.empty(10, dtype=np.float32)
+    rc = _abi.lib.fvsr_rope_tables(10000.0, out.ctypes.data_as(C.c_void_p), 10)
+    assert rc == _abi.ERR_INVALID_ARG
