@@ -172,6 +172,18 @@ int fvsr_kv_ring_append_qkv(fvsr_kv_ring* ring, int layer, const void* q, const 
                             int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
                             const float* rope_tables, void* q_out, void* stream);
 
+/* The LCSA layer call from the projections: the self-attention core of `blockForward` (DiT.swift:496-539) between
+ * the q/k/v projections and the o projection. fvsr_kv_ring_append_qkv (normQ/normK + RoPE + window partition +
+ * cache append), selection over cache ++ new, attention (mode AUTO: threshold 0.45), evict; the attention output
+ * is written in natural (f, h, w) token order, i.e. the reference's windowReverse (DiT.swift:121-126,539) is fused
+ * into the attention kernel's store. q, k, v: (2*n_new_slices*8bh*8bw, C) projections in natural order; q_work:
+ * (same shape) receives q' in window order; o: (same shape) the attention output in natural order. The queries
+ * are the chunk's own n_new_slices slices. mask_out/probs_out may be NULL. */
+int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const void* q, const void* k, const void* v,
+                        int n_new_slices, int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                        const float* rope_tables, const uint8_t* local_dev, int topk, int mode, void* q_work, void* o,
+                        float* mask_out, float* probs_out, void* stream);
+
 /* ---- (a1) window layout ------------------------------------------------------------------------------------ */
 /* Replace `windowPartition` / `windowReverse` (DiT.swift:113-126): (f*h*w, C) natural <-> window order. */
 int fvsr_window_partition(int dtype, const void* x, void* out, int f, int h, int w, int channels, void* stream);

@@ -577,11 +577,15 @@ int fvsr_lcsa_select_ring(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void*
 
 static int attention_ring_impl(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q, int64_t lq,
                                const int32_t* kidx, const int32_t* kcnt, int nk_stride, const uint8_t* sel,
-                               bool dense, void* o, hipStream_t stream) {
+                               bool dense, void* o, hipStream_t stream, bool o_grid = false) {
   const int nk = r->count[layer] * r->s;
   AttnArgs a = make_args(q, lq, r->layer_k(layer), r->layer_v(layer), (int64_t)nk * kBlock, r->heads, kidx, kcnt,
                          sel, nk_stride, nk, r->map(layer), o);
   a.kv_rows = (int64_t)r->layer_tokens();
+  if (o_grid) {   // whole windows of the ring's (8 bh, 8 bw) grid: write o in natural token order
+    a.o_nbh = r->bh;
+    a.o_nbw = r->bw;
+  }
   int rc = attach_order(ctx, a, nk);
   if (rc) return rc;
   return launch_attention(r->dtype, dense, a, stream);
@@ -646,6 +650,47 @@ int fvsr_lcsa_layer(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* qW, i
   int use = mode;
   if (use == FVSR_ATTN_AUTO) fvsr_attention_mode_auto(topk, r->s, nk, kAutoThreshold, nullptr, &use);
   rc = attention_ring_impl(ctx, r, layer, qW, lq, kidx, kcnt, nk, sel, use == FVSR_ATTN_DENSE, o, st);
+  if (rc) return rc;
+  return fvsr_kv_ring_evict(r, layer);
+}
+
+int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q, const void* k, const void* v,
+                        int n_new_slices, int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                        const float* rope_tables, const uint8_t* local_dev, int topk, int mode, void* q_work, void* o,
+                        float* mask_out, float* probs_out, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  FVSR_REQUIRE(q_work && o && local_dev, FVSR_ERR_INVALID_ARG, "q_work, o and local must be non-NULL");
+  FVSR_REQUIRE(mode == FVSR_ATTN_AUTO || mode == FVSR_ATTN_KERNEL || mode == FVSR_ATTN_DENSE,
+               FVSR_ERR_INVALID_ARG, "bad attention mode");
+  FVSR_REQUIRE(n_new_slices > 0 && topk >= 0, FVSR_ERR_INVALID_ARG, "n_new_slices must be > 0, topk >= 0");
+  FVSR_REQUIRE(r->count[layer] + n_new_slices <= r->capacity, FVSR_ERR_CAPACITY,
+               "append would exceed the ring capacity");
+  const int nk_after = (r->count[layer] + n_new_slices) * r->s;
+  FVSR_REQUIRE(nk_after <= kMaxSelectKeyBlocks, FVSR_ERR_UNSUPPORTED, "too many key blocks for selection");
+  hipStream_t st = (hipStream_t)stream;
+  // the chunk's queries: q_slices = n_new_slices slices of s windows (DiT.swift:478-485: seqlen = f / 2)
+  const int q_slices = n_new_slices;
+  const int64_t lq = (int64_t)q_slices * r->s * kBlock;
+  const int64_t nq = (int64_t)q_slices * r->s;
+  const Carve cv = carve(r->heads, nq, nk_after, r->C);
+  if ((rc = ensure_ws(ctx, cv.total))) return rc;
+  if ((rc = fvsr_kv_ring_append_qkv(r, layer, q, k, v, n_new_slices, t0, norm_q_weight, norm_k_weight, eps,
+                                    rope_tables, q_work, stream)))
+    return rc;
+  const int nk = r->count[layer] * r->s;
+  char* ws = (char*)ctx->ws;
+  int32_t* kidx = (int32_t*)(ws + cv.kidx);
+  int32_t* kcnt = (int32_t*)(ws + cv.kcnt);
+  uint8_t* sel = (uint8_t*)(ws + cv.sel);
+  rc = select_impl(ctx, r->dtype, q_work, lq, r->layer_pooled(layer), true, nullptr, (int64_t)nk * kBlock,
+                   r->map(layer), nk, r->heads, q_slices, r->s, local_dev, topk, mask_out, probs_out, kidx, kcnt,
+                   sel, st);
+  if (rc) return rc;
+  int use = mode;
+  if (use == FVSR_ATTN_AUTO) fvsr_attention_mode_auto(topk, r->s, nk, kAutoThreshold, nullptr, &use);
+  rc = attention_ring_impl(ctx, r, layer, q_work, lq, kidx, kcnt, nk, sel, use == FVSR_ATTN_DENSE, o, st, true);
   if (rc) return rc;
   return fvsr_kv_ring_evict(r, layer);
 }

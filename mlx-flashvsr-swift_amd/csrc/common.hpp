@@ -76,6 +76,10 @@ struct AttnArgs {
   float c;               // softmax scale * log2(e)
   int32_t* order;        // (H * nq) rows, longest key list first (bf16 persistent walk; workspace)
   int32_t* counter;      // next index into `order` (workspace; zeroed by the order kernel)
+  int o_nbh, o_nbw;      // > 0: write o in natural (f, h, w) token order of an (8 o_nbh, 8 o_nbw) grid (the
+                         // reference's windowReverse, DiT.swift:121-126) instead of window order
+  // output row of window-order query row r
+  __device__ __forceinline__ int64_t out_row(int64_t r) const;
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -89,6 +93,10 @@ __device__ __forceinline__ int64_t window_token_to_grid(int b, int t, int nbh, i
   const int wf = t >> 6, wh = (t >> 3) & 7, ww = t & 7;
   const int64_t H = 8 * nbh, W = 8 * nbw;
   return ((int64_t)(2 * nf + wf) * H + 8 * nh + wh) * W + 8 * nw + ww;
+}
+
+__device__ __forceinline__ int64_t AttnArgs::out_row(int64_t r) const {
+  return o_nbw > 0 ? window_token_to_grid((int)(r >> 7), (int)(r & 127), o_nbh, o_nbw) : r;
 }
 
 }  // namespace fvsr

@@ -176,7 +176,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   if (cnt <= 0) {   // empty query block -> zeros (SparseAttention.swift:47-53; DiT.swift:300-304)
     for (int e = tid; e < kBlock * 16; e += kThreads) {
       const int64_t row = (int64_t)qb * kBlock + (e >> 4);
-      if (row < a.lq) *(u32x4*)(O + row * a.ld + hc + (e & 15) * 8) = u32x4{0, 0, 0, 0};
+      if (row < a.lq) *(u32x4*)(O + a.out_row(row) * a.ld + hc + (e & 15) * 8) = u32x4{0, 0, 0, 0};
     }
     continue;
   }
@@ -551,7 +551,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int64_t qrow = (int64_t)qb * kBlock + wave * kQW + q * 32 + l32;
     if (qrow < a.lq) {
-      bf16* orow = O + qrow * a.ld + hc;
+      bf16* orow = O + a.out_row(qrow) * a.ld + hc;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -637,7 +637,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnArgs a) {
   if (cnt <= 0) {
     for (int e = tid; e < kBlock * 32; e += 256) {
       const int64_t row = (int64_t)qb * kBlock + (e >> 5);
-      if (row < a.lq) *(f32x4*)(O + row * a.ld + hc + (e & 31) * 4) = f32x4{0, 0, 0, 0};
+      if (row < a.lq) *(f32x4*)(O + a.out_row(row) * a.ld + hc + (e & 31) * 4) = f32x4{0, 0, 0, 0};
     }
     return;
   }
@@ -759,7 +759,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnArgs a) {
   const float l_tot = pair_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qrow < a.lq) {
-    float* orow = O + qrow * a.ld + hc;
+    float* orow = O + a.out_row(qrow) * a.ld + hc;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll

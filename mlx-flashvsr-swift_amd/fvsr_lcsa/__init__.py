@@ -324,6 +324,27 @@ class KVRing:
              _ptr(wk), float(eps), _ptr(tab), _ptr(qo), _stream(stream))
         return qo
 
+    def layer_call_qkv(self, layer: int, q, k, v, n_new_slices: int, t0: int, norm_q_weight, norm_k_weight, local,
+                       topk: int, mode: int = ATTN_AUTO, eps: float = 1e-6, theta: float = 10000.0, stream=None,
+                       out=None, q_work=None, want_mask=False, want_probs=False):
+        """The LCSA layer call from the projections (DiT.swift:496-539): epilogue into the ring, select, attend,
+        evict; returns (o in natural token order, mask, probs)."""
+        q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+        wq = norm_q_weight.to(q2.dtype).contiguous()
+        wk = norm_k_weight.to(q2.dtype).contiguous()
+        tab = rope_tables_device(q2.device, theta)
+        qw = torch.empty_like(q2) if q_work is None else _tokens(q_work, "q_work")
+        o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+        nq = n_new_slices * self.s
+        nk = (self.slices(layer) + n_new_slices) * self.s
+        dev = q2.device
+        mask = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_mask else None
+        probs = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
+        call("fvsr_lcsa_layer_qkv", self.ctx.handle, self.handle, layer, _ptr(q2), _ptr(k2), _ptr(v2), n_new_slices,
+             t0, _ptr(wq), _ptr(wk), float(eps), _ptr(tab), _ptr(self.ctx.local_device(local)), topk, mode,
+             _ptr(qw), _ptr(o), _ptr(mask), _ptr(probs), _stream(stream))
+        return o, mask, probs
+
     def evict(self, layer: int):
         call("fvsr_kv_ring_evict", self.handle, layer)
 

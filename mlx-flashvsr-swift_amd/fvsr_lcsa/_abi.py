@@ -47,6 +47,8 @@ SIGNATURES = {
     "fvsr_qkv_epilogue": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp,
                                _vp]),
     "fvsr_kv_ring_append_qkv": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _vp]),
+    "fvsr_lcsa_layer_qkv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _i, _i, _vp,
+                                 _vp, _vp, _vp, _vp]),
     "fvsr_window_partition": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "fvsr_window_reverse": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
 }

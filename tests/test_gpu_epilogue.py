@@ -123,3 +123,27 @@ def test_ring_append_qkv_wrapping_append(dev):
             window_k.pop(0)
             window_v.pop(0)
     ring.close()
+
+
+@pytest.mark.parametrize("bh,bw,heads", [(3, 4, 12), (9, 15, 12)])
+def test_layer_call_from_projections_equals_manual_sequence(dev, bh, bw, heads):
+    """fvsr_lcsa_layer_qkv (epilogue into the ring, select, attend, evict, output in natural order) equals the plain
+    epilogue followed by the window-order layer call and a window reverse, bit for bit, over chunk 0 (3 slices) and
+    two streaming chunks."""
+    h, w, s = 8 * bh, 8 * bw, bh * bw
+    local = fvsr_lcsa.local_block_mask(bh, bw, 11)
+    ring_a = fvsr_lcsa.KVRing(1, heads, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    ring_b = fvsr_lcsa.KVRing(1, heads, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    for n, t0, seed in ((3, 0, 31), (1, 6, 32), (1, 8, 33)):
+        f = 2 * n
+        q, k, v, wq, wk = (t.to(dev) for t in _inputs(f, h, w, heads, torch.bfloat16, seed))
+        topk = int(s * s * 0.5) - 1
+        o_a, m_a, _ = ring_a.layer_call_qkv(0, q, k, v, n, t0, wq, wk, local, topk, want_mask=True)
+        qp, kp, vp = fvsr_lcsa.qkv_epilogue(q, k, v, f, h, w, heads, t0, wq, wk)
+        o_b, m_b, _ = ring_b.layer_call(0, qp, kp, vp, n, n, local, topk, want_mask=True)
+        torch.cuda.synchronize()
+        assert torch.equal(m_a, m_b)
+        assert torch.equal(o_a, fvsr_lcsa.window_reverse(o_b, f, h, w))
+        assert ring_a.slices(0) == ring_b.slices(0)
+    ring_a.close()
+    ring_b.close()
