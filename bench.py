@@ -45,6 +45,9 @@ def parse_args():
                          "6-latent-frame first chunk and 4 chunks of 2 latent frames; append + select + attention + "
                          "evict per layer call; prints its own JSON line")
     ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--from-projections", action="store_true",
+                    help="with --stream: feed each layer the q/k/v projections in natural token order "
+                         "(normQ/normK + RoPE + window partition + ring append fused, output window-reversed)")
     ap.add_argument("--epilogue", action="store_true",
                     help="time the fused QKV epilogue into the KV ring on one 1920x1152 streaming chunk (HBM-bound)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -156,10 +159,16 @@ def stream_bench(args):
     chunks = [(3, 0), (1, 6), (1, 8), (1, 10), (1, 12)]   # (slices, first latent frame)
     gen = torch.Generator(device=dev).manual_seed(args.seed)
     data = []
+    proj = args.from_projections
+    wq = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
+    wk = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
     for n, t0 in chunks:
         f = 2 * n
         L = f * lat_h * lat_w
         q, k, v = (torch.randn((L, C), generator=gen, device=dev) for _ in range(3))
+        if proj:   # the projections themselves, natural token order; the layer call normalises and rotates
+            data.append(tuple(x.to(torch.bfloat16).contiguous() for x in (q, k, v)))
+            continue
         cos, sin = synth.rope_grid(f, lat_h, lat_w, t0, device=dev)
         q = synth.rope_apply(synth.rms_norm(q, H), H, cos, sin)
         k = synth.rope_apply(synth.rms_norm(k, H), H, cos, sin)
@@ -167,20 +176,29 @@ def stream_bench(args):
                           for x in (q, k, v)))
     ring = fvsr_lcsa.KVRing(args.layers, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
     outs = [torch.empty_like(d[0]) for d in data]
+    qwork = [torch.empty_like(d[0]) for d in data]
+
+    def call(layer, c, want_mask=False):
+        (n, t0), (q, k, v), o = chunks[c], data[c], outs[c]
+        if proj:
+            return ring.layer_call_qkv(layer, q, k, v, n, t0, wq, wk, local, topk, out=o, q_work=qwork[c],
+                                       want_mask=want_mask)
+        return ring.layer_call(layer, q, k, v, n, n, local, topk, out=o, want_mask=want_mask)
+
     # kept block pairs per chunk (untimed; the same data feeds every layer)
     kept_pairs = []
-    for (n, _), (q, k, v), o in zip(chunks, data, outs):
-        _, m, _ = ring.layer_call(0, q, k, v, n, n, local, topk, out=o, want_mask=True)
+    for c in range(len(chunks)):
+        _, m, _ = call(0, c, want_mask=True)
         kept_pairs.append(float(m.sum().item()))
     ring.reset()
 
     def run_stream(events=None):
         ring.reset()
-        for c, ((n, _), (q, k, v), o) in enumerate(zip(chunks, data, outs)):
+        for c in range(len(chunks)):
             if events is not None:
                 events[c][0].record()
             for layer in range(args.layers):
-                ring.layer_call(layer, q, k, v, n, n, local, topk, out=o)
+                call(layer, c)
             if events is not None:
                 events[c][1].record()
 
@@ -198,14 +216,16 @@ def stream_bench(args):
     flops = [4.0 * 128 ** 3 * p * args.layers for p in kept_pairs]
     steady = tot[1:]
     line = {
-        "metric": "LCSA attention stack per streaming chunk, 1920x1152 (append + select + attention + evict)",
+        "metric": ("LCSA attention stack per streaming chunk, 1920x1152 (q/k/v projections -> norm + RoPE + window "
+                   "partition + append + select + attention + evict + window reverse)" if proj else
+                   "LCSA attention stack per streaming chunk, 1920x1152 (append + select + attention + evict)"),
         "unit": "ms per chunk (all layers)",
         "value": round(sum(steady) / len(steady), 3),
         "higher_is_better": False,
         "n_gpus": 1,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1), per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)",
-        "config": {"workload": "stream_1920x1152_bf16", "layers": args.layers, "heads": H, "head_dim": 128,
+        "config": {"workload": "stream_1920x1152_bf16" + ("_from_projections" if proj else ""), "layers": args.layers, "heads": H, "head_dim": 128,
                    "spatial_blocks_per_slice": s, "local_range": 11, "topk": topk, "kv_window_slices": 3,
                    "chunks": [{"query_blocks": n * s, "key_blocks": min(n + (3 if c else 0), 4) * s}
                               for c, (n, _) in enumerate(chunks)]},
