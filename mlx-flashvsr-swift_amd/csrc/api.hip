@@ -27,7 +27,6 @@ int launch_lists_from_mask(const float* mask, int rows, int nk, int32_t* kidx, i
                            hipStream_t stream);
 int launch_sel_from_lists(const int32_t* kidx, const int32_t* kcnt, int rows, int nk_stride, int nk, uint8_t* sel,
                           hipStream_t stream);
-int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream);
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
                           const uint8_t* local, float* probs, unsigned* hist, int q_slices, hipStream_t stream);
 size_t hist12_bytes(int heads, int q_slices);
@@ -36,9 +35,8 @@ int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices
 int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int C, int t0,
                         const void* wq, const void* wk, float eps, const float* rope, void* q_out, void* k_out,
                         void* v_out, int dst_slot0, int capacity, int slice_blocks, hipStream_t stream);
-int launch_pool_parts(int dtype, const void* x, int64_t L, int C, float* partial, hipStream_t stream);
-int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
-                       int slice_blocks, float* out, hipStream_t stream);
+int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream);
+int launch_pool_finish(const PoolDst* dst, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream);
 int rope_table_floats();
 void rope_tables_host(double theta, float* out);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
@@ -49,7 +47,7 @@ int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* 
 int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int w, int C, bool to_windows,
                          hipStream_t stream);
 
-constexpr int kMaxSelectKeyBlocks = 1920;    // scores stage keeps (8 x (128 + Nk)) fp32 in 64 KB of LDS
+constexpr int kMaxSelectKeyBlocks = 1920;    // scores stage: (8 x (128 + Nk) + 64 x 132) fp32 + 32 KB in LDS
 constexpr double kAutoThreshold = 0.45;      // DiT.swift:210
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -70,7 +68,7 @@ static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   c.order = off; off += align256((size_t)heads * nq * 4);
   c.counter = off; off += 256;
   c.thr = off; off += align256((size_t)heads * nq * 4);   // per (head, query slice) thresholds (nq >= slices)
-  c.partial = off; off += align256((size_t)std::max(nq, nk) * kPoolParts * C * 4);   // pooling runs
+  c.partial = off; off += align256((size_t)(nq + nk) * kPoolParts * C * 4);   // pooling runs of Q, then K
   c.hist = off; off += align256(hist12_bytes(heads, (int)nq));   // nq >= query slices
   c.total = off;
   return c;
@@ -209,10 +207,12 @@ int fvsr_attention_mode_auto(int topk, int s, int nk, double threshold, double* 
 // ---------------------------------------------------------------------------------------------------------------
 // selection
 // ---------------------------------------------------------------------------------------------------------------
+// q_pooled: the caller has already written the pooled queries to the workspace's pq and cleared its histogram
+// (the qkv layer call does both in the launches of its ring append)
 static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const float* pk_src, bool pk_ready,
                        const void* kW, int64_t lk, KeyMap kmap, int nk, int heads, int q_slices, int s,
                        const uint8_t* local, int topk, float* mask_out, float* probs_out, int32_t* kidx,
-                       int32_t* kcnt, uint8_t* sel_out, hipStream_t stream) {
+                       int32_t* kcnt, uint8_t* sel_out, hipStream_t stream, bool q_pooled = false) {
   const int C = heads * kHeadDim;
   const int64_t nq = ceil_div(lq, kBlock);
   FVSR_REQUIRE(nq == (int64_t)q_slices * s, FVSR_ERR_INVALID_ARG,
@@ -229,14 +229,28 @@ static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, con
   uint8_t* sel = sel_out ? sel_out : (uint8_t*)(ws + cv.sel);
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   float* partial = (float*)(ws + cv.partial);
-  if ((rc = launch_pool(dtype, qW, lq, C, pq, partial, stream))) return rc;
-  const float* pk = pk_src;
-  if (!pk_ready) {
-    float* pkw = (float*)(ws + cv.pk);
-    if ((rc = launch_pool(dtype, kW, lk, C, pkw, partial, stream))) return rc;
-    pk = pkw;
-  }
   unsigned* hist = (unsigned*)(ws + cv.hist);
+  const float* pk = pk_ready ? pk_src : (const float*)(ws + cv.pk);
+  if (!q_pooled || !pk_ready) {
+    // block sums of Q (and K) in one launch, then the block means and the histogram reset in one more
+    PoolSrc src[2];
+    PoolDst dst[2];
+    int n = 0;
+    float* kpart = partial + (size_t)nq * kPoolParts * C;
+    if (!q_pooled) {
+      src[n] = PoolSrc{qW, partial, lq, 0};
+      dst[n++] = PoolDst{partial, pq, lq, 0, 0, 1, 1 << 30};
+    }
+    if (!pk_ready) {
+      src[n] = PoolSrc{kW, kpart, lk, 0};
+      dst[n++] = PoolDst{kpart, (float*)(ws + cv.pk), lk, 0, 0, 1, 1 << 30};
+    }
+    if ((rc = launch_pool_parts(dtype, src, n, C, stream))) return rc;
+    for (int i = 0; i < n; ++i) dst[i].nb = src[i].nb;
+    if ((rc = launch_pool_finish(dst, n, C, q_pooled ? nullptr : hist,
+                                 (int64_t)(hist12_bytes(heads, q_slices) / sizeof(unsigned)), stream)))
+      return rc;
+  }
   if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, hist, q_slices, stream)))
     return rc;
   return launch_topk_emit(probs, heads, (int)nq, nk, q_slices, topk, hist, (float*)(ws + cv.thr), mask_out, sel,
@@ -492,9 +506,15 @@ int fvsr_kv_ring_append(fvsr_kv_ring* r, int layer, const void* k_new, const voi
   return FVSR_OK;
 }
 
-int fvsr_kv_ring_append_qkv(fvsr_kv_ring* r, int layer, const void* q, const void* k, const void* v, int n_slices,
-                            int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
-                            const float* rope_tables, void* q_out, void* stream) {
+}  // extern "C"
+
+// The ring append of fvsr_kv_ring_append_qkv. With q_pool set (the layer call), the block sums of the written
+// queries ride in the same pool_part launch as the new keys' (q_pool->partial, its own scratch), their means go
+// to q_pooled in the same pool_finish launch, which also clears the selection histogram `hist` (nhist words).
+static int append_qkv_impl(fvsr_kv_ring* r, int layer, const void* q, const void* k, const void* v, int n_slices,
+                           int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                           const float* rope_tables, void* q_out, hipStream_t stream, float* q_partial = nullptr,
+                           float* q_pooled = nullptr, unsigned* hist = nullptr, int64_t nhist = 0) {
   int rc = check_layer(r, layer);
   if (rc) return rc;
   FVSR_REQUIRE(n_slices > 0, FVSR_ERR_INVALID_ARG, "n_slices must be > 0");
@@ -510,25 +530,37 @@ int fvsr_kv_ring_append_qkv(fvsr_kv_ring* r, int layer, const void* q, const voi
   const int nb = n_slices * r->s;
   rc = launch_qkv_epilogue(r->dtype, q, k, v, 2 * n_slices, 8 * r->bh, 8 * r->bw, r->C, t0, norm_q_weight,
                            norm_k_weight, eps, rope_tables, q_out, r->layer_k(layer), r->layer_v(layer), slot0,
-                           r->capacity, r->s, (hipStream_t)stream);
+                           r->capacity, r->s, stream);
   if (rc) return rc;
   // pooled keys of the new slots, as for plain buffers: block sums over the slots up to the end of the ring, then
-  // the wrapped remainder from slot 0
+  // the wrapped remainder from slot 0 (and the queries'), one launch
   const int first = std::min(n_slices, r->capacity - slot0);
   const size_t slot_bytes = (size_t)r->s * kBlock * r->C * esize(r->dtype);
-  rc = launch_pool_parts(r->dtype, r->layer_k(layer) + slot0 * slot_bytes, (int64_t)first * r->s * kBlock, r->C,
-                         r->partial, (hipStream_t)stream);
-  if (rc) return rc;
-  if (first < n_slices) {
-    rc = launch_pool_parts(r->dtype, r->layer_k(layer), (int64_t)(n_slices - first) * r->s * kBlock, r->C,
-                           r->partial + (size_t)first * r->s * kPoolParts * r->C, (hipStream_t)stream);
-    if (rc) return rc;
-  }
-  rc = launch_pool_finish(r->partial, nb, r->C, (int64_t)nb * kBlock, slot0, r->capacity, r->s,
-                          r->layer_pooled(layer), (hipStream_t)stream);
-  if (rc) return rc;
+  const int64_t lq = (int64_t)nb * kBlock;
+  PoolSrc src[3];
+  int ns = 0;
+  src[ns++] = PoolSrc{r->layer_k(layer) + slot0 * slot_bytes, r->partial, (int64_t)first * r->s * kBlock, 0};
+  if (first < n_slices)
+    src[ns++] = PoolSrc{r->layer_k(layer), r->partial + (size_t)first * r->s * kPoolParts * r->C,
+                        (int64_t)(n_slices - first) * r->s * kBlock, 0};
+  if (q_partial) src[ns++] = PoolSrc{q_out, q_partial, lq, 0};
+  if ((rc = launch_pool_parts(r->dtype, src, ns, r->C, stream))) return rc;
+  PoolDst dst[2];
+  int nd = 0;
+  dst[nd++] = PoolDst{r->partial, r->layer_pooled(layer), lq, nb, slot0, r->capacity, r->s};
+  if (q_partial) dst[nd++] = PoolDst{q_partial, q_pooled, lq, nb, 0, 1, 1 << 30};
+  if ((rc = launch_pool_finish(dst, nd, r->C, hist, nhist, stream))) return rc;
   r->count[layer] += n_slices;
   return FVSR_OK;
+}
+
+extern "C" {
+
+int fvsr_kv_ring_append_qkv(fvsr_kv_ring* r, int layer, const void* q, const void* k, const void* v, int n_slices,
+                            int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
+                            const float* rope_tables, void* q_out, void* stream) {
+  return append_qkv_impl(r, layer, q, k, v, n_slices, t0, norm_q_weight, norm_k_weight, eps, rope_tables, q_out,
+                         (hipStream_t)stream);
 }
 
 int fvsr_kv_ring_evict(fvsr_kv_ring* r, int layer) {
@@ -676,17 +708,19 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q
   const int64_t nq = (int64_t)q_slices * r->s;
   const Carve cv = carve(r->heads, nq, nk_after, r->C);
   if ((rc = ensure_ws(ctx, cv.total))) return rc;
-  if ((rc = fvsr_kv_ring_append_qkv(r, layer, q, k, v, n_new_slices, t0, norm_q_weight, norm_k_weight, eps,
-                                    rope_tables, q_work, stream)))
+  char* ws = (char*)ctx->ws;
+  // the pooled queries and the histogram reset ride in the append's pooling launches
+  if ((rc = append_qkv_impl(r, layer, q, k, v, n_new_slices, t0, norm_q_weight, norm_k_weight, eps, rope_tables,
+                            q_work, st, (float*)(ws + cv.partial), (float*)(ws + cv.pq), (unsigned*)(ws + cv.hist),
+                            (int64_t)(hist12_bytes(r->heads, q_slices) / sizeof(unsigned)))))
     return rc;
   const int nk = r->count[layer] * r->s;
-  char* ws = (char*)ctx->ws;
   int32_t* kidx = (int32_t*)(ws + cv.kidx);
   int32_t* kcnt = (int32_t*)(ws + cv.kcnt);
   uint8_t* sel = (uint8_t*)(ws + cv.sel);
   rc = select_impl(ctx, r->dtype, q_work, lq, r->layer_pooled(layer), true, nullptr, (int64_t)nk * kBlock,
                    r->map(layer), nk, r->heads, q_slices, r->s, local_dev, topk, mask_out, probs_out, kidx, kcnt,
-                   sel, st);
+                   sel, st, true);
   if (rc) return rc;
   int use = mode;
   if (use == FVSR_ATTN_AUTO) fvsr_attention_mode_auto(topk, r->s, nk, kAutoThreshold, nullptr, &use);

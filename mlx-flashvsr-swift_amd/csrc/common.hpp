@@ -55,6 +55,25 @@ struct KeyMap {
   }
 };
 
+// One block-pooling source of pool_part_kernel (lcsa_select.hip): the fp32 sums of the runs of 32 tokens of the L
+// tokens of x (nb = ceil(L / 128) blocks) go to partial[(b * kPoolParts + part) * C + c].
+struct PoolSrc {
+  const void* x;
+  float* partial;
+  int64_t L;
+  int nb;
+};
+
+// One block-mean target of pool_finish_kernel (kv_ring.hip): nb blocks (L tokens) of run sums in partial; block b
+// is written to row ((slot0 + b / slice_blocks) % capacity) * slice_blocks + b % slice_blocks of out (a ring
+// slot mapping; slot0 0, capacity 1, slice_blocks >= nb for a plain buffer).
+struct PoolDst {
+  const float* partial;
+  float* out;
+  int64_t L;
+  int nb, slot0, capacity, slice_blocks;
+};
+
 // Arguments of the attention kernels (lcsa_attn.hip).
 struct AttnArgs {
   const void* q;

@@ -57,25 +57,35 @@ __global__ void block_copy_kernel(const T* __restrict__ src, T* __restrict__ dst
 
 // Block means from the per-run sums: out[dst(b) * C + c] = ((p0 + p1) + (p2 + p3)) / n_b, n_b = the valid tokens
 // of block b (L tokens in all), dst(b) the ring mapping of block_copy_kernel (identity for plain buffers). The fixed
-// order makes the pooled keys of a ring append and of a plain-buffer pool bit-identical.
-__global__ void pool_finish_kernel(const float* __restrict__ partial, int nb, int C, int64_t L, int dst_slot0,
-                                   int capacity, int slice_blocks, float* __restrict__ out) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= (int64_t)nb * C) return;
+// order makes the pooled keys of a ring append and of a plain-buffer pool bit-identical. One launch finishes up to
+// two targets (d0's elements first) and also clears `zero` (nzero words), the selection's histogram, which saves a
+// launch of its own.
+__global__ void pool_finish_kernel(PoolDst d0, PoolDst d1, int C, unsigned* __restrict__ zero, int64_t nzero) {
+  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < nzero) zero[e] = 0u;
+  PoolDst d = d0;
+  const int64_t n0 = (int64_t)d0.nb * C;
+  if (e >= n0) {
+    e -= n0;
+    d = d1;
+  }
+  if (e >= (int64_t)d.nb * C) return;
   const int b = (int)(e / C), c = (int)(e - (int64_t)b * C);
-  const float* p = partial + (int64_t)b * kPoolParts * C + c;
+  const float* p = d.partial + (int64_t)b * kPoolParts * C + c;
   const float sum = (p[0] + p[C]) + (p[2 * C] + p[3 * C]);
-  const int n = (int)min<int64_t>(kBlock, L - (int64_t)b * kBlock);
-  const int64_t db = (int64_t)((dst_slot0 + b / slice_blocks) % capacity) * slice_blocks + (b % slice_blocks);
-  out[db * C + c] = sum / (float)n;
+  const int n = (int)min<int64_t>(kBlock, d.L - (int64_t)b * kBlock);
+  const int64_t db = (int64_t)((d.slot0 + b / d.slice_blocks) % d.capacity) * d.slice_blocks + (b % d.slice_blocks);
+  d.out[db * C + c] = sum / (float)n;
 }
 
-int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
-                       int slice_blocks, float* out, hipStream_t stream) {
-  const int64_t n = (int64_t)nb * C;
-  if (n <= 0) return FVSR_OK;
-  hipLaunchKernelGGL(pool_finish_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, stream, partial, nb, C, L,
-                     dst_slot0, capacity, slice_blocks, out);
+// n targets (0..2); zero / nzero may be null / 0
+int launch_pool_finish(const PoolDst* dst, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream) {
+  PoolDst d[2] = {};
+  for (int i = 0; i < n && i < 2; ++i) d[i] = dst[i];
+  const int64_t total = std::max((int64_t)d[0].nb * C + (int64_t)d[1].nb * C, zero ? nzero : 0);
+  if (total <= 0) return FVSR_OK;
+  hipLaunchKernelGGL(pool_finish_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, stream, d[0], d[1], C,
+                     zero, zero ? nzero : 0);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }
@@ -118,7 +128,8 @@ int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_bl
                        (const float*)v_new, (float*)ring_v);
   }
   FVSR_HIP_CHECK(hipGetLastError());
-  return launch_pool_finish(partial, n_blocks, C, (int64_t)n_blocks * kBlock, slot0, capacity, s, pooled, stream);
+  const PoolDst d{partial, pooled, (int64_t)n_blocks * kBlock, n_blocks, slot0, capacity, s};
+  return launch_pool_finish(&d, 1, C, nullptr, 0, stream);
 }
 
 int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,

@@ -9,15 +9,18 @@
 //   k = min(n - 1, topk).
 //
 // Kernels (all HBM/L2-bound, no MFMA — the score product is 0.1 GFLOP):
-//   pool_part_kernel     one workgroup per run of 32 tokens of a block: coalesced 16-byte loads, fp32 sums; the
-//                        means come from pool_finish_kernel (kv_ring.hip) in a fixed order
-//   scores_softmax_kernel one workgroup per (8 query blocks, head): pooled-key rows read once per 8 query rows,
-//                         scores + local mask staged in LDS, one wave per row for max / exp / sum / normalise
-//   scores_softmax_kernel also counts the nonzero probs of each (head, query slice) per top-12-bit bin
+//   pool_part_kernel     one workgroup per run of 32 tokens of a block: coalesced 16-byte loads, fp32 sums (Q
+//                        and K, or Q and the new ring keys, in one launch); the means come from pool_finish_kernel
+//                        (kv_ring.hip) in a fixed order, which also clears the histogram below
+//   scores_softmax_kernel one workgroup per (8 query blocks, head): pooled-key rows staged through LDS in coalesced
+//                         chunks of 64 keys and read once per 8 query rows, scores + local mask in LDS, one wave per
+//                         row for max / exp / sum / normalise; it also counts the nonzero probs of each (head,
+//                         query slice) per top-12-bit bin
 //   topk_threshold_kernel one 1024-thread workgroup per (head, query slice): exact (k+1)-th largest over the fp32
-//                         bit patterns (probs are >= 0, so bit order = value order): the histogram picks the bin,
-//                         its elements are gathered to LDS and three radix passes finish the low 19 bits (full-row
-//                         4-pass radix select when the bin is too large)
+//                         bit patterns (probs are >= 0, so bit order = value order): the row is loaded into
+//                         registers at once, the histogram picks the bin, its elements are gathered to LDS and
+//                         three radix passes finish the low 19 bits (full-row 4-pass radix select when the bin is
+//                         too large)
 //   topk_emit_kernel     one wave per query row: mask, selection bytes and compacted key lists (ballot + popcount)
 #include "common.hpp"
 
@@ -39,16 +42,29 @@ struct Vec16<bf16> {
   typedef bf16x8 type;
 };
 
-// x: (L, C) tokens; grid (nb, kPoolParts): run `part` of block b sums rows [b*128 + 32*part, +32) that exist into
-// partial[(b * kPoolParts + part) * C + c] (fp32); pool_finish_kernel forms the block means.
+// Sources s0, s1, s2 ((L, C) tokens each) share one launch: grid (s0.nb + s1.nb + s2.nb, kPoolParts), block
+// index b of the grid runs over s0's blocks, then s1's, then s2's. Run `part` of block b sums rows
+// [b*128 + 32*part, +32) that exist into partial[(b * kPoolParts + part) * C + c] (fp32); pool_finish_kernel forms
+// the block means.
 template <typename T>
-__global__ void pool_part_kernel(const T* __restrict__ x, int64_t L, int C, float* __restrict__ partial) {
+__global__ void pool_part_kernel(PoolSrc s0, PoolSrc s1, PoolSrc s2, int C) {
   constexpr int VN = Vec16<T>::N;
   constexpr int kRun = kBlock / kPoolParts;
   typedef typename Vec16<T>::type VT;
-  const int b = blockIdx.x, part = blockIdx.y;
+  int b = blockIdx.x;
+  const int part = blockIdx.y;
+  PoolSrc src = s0;
+  if (b >= s0.nb) {
+    b -= s0.nb;
+    src = s1;
+    if (b >= s1.nb) {
+      b -= s1.nb;
+      src = s2;
+    }
+  }
+  const T* __restrict__ x = (const T*)src.x;
   const int64_t r0 = (int64_t)b * kBlock + part * kRun;
-  const int n = (int)max<int64_t>(0, min<int64_t>(kRun, L - r0));
+  const int n = (int)max<int64_t>(0, min<int64_t>(kRun, src.L - r0));
   const int nvec = C / VN;
   for (int cv = threadIdx.x; cv < nvec; cv += blockDim.x) {
     float acc[VN];
@@ -61,16 +77,38 @@ __global__ void pool_part_kernel(const T* __restrict__ x, int64_t L, int C, floa
 #pragma unroll
       for (int e = 0; e < VN; ++e) acc[e] += (float)v[e];
     }
-    float* o = partial + ((int64_t)b * kPoolParts + part) * C + cv * VN;
+    float* o = src.partial + ((int64_t)b * kPoolParts + part) * C + cv * VN;
 #pragma unroll
     for (int e = 0; e < VN; ++e) o[e] = acc[e];
   }
 }
 
+// Adds 1 to h[key] for every lane with `valid`; must be called by all 64 lanes of the wave together. Lanes with
+// equal keys are merged first (up to kPeel distinct keys, each by one atomic of the group's size from its lowest
+// lane): probs that cluster in a few bins would otherwise put up to 64 atomics on one LDS address, which execute
+// one after another. Keys left after the merge rounds (a spread-out wave) take one atomic per lane.
+constexpr int kPeel = 4;
+__device__ __forceinline__ void wave_hist_add(unsigned* h, unsigned key, bool valid) {
+  const int lane = threadIdx.x & 63;
+  uint64_t todo = __ballot(valid);
+#pragma unroll
+  for (int it = 0; it < kPeel; ++it) {
+    if (todo == 0ull) break;   // wave-uniform
+    const int leader = __builtin_ctzll(todo);
+    const unsigned lkey = (unsigned)__builtin_amdgcn_readlane((int)key, leader);
+    const uint64_t grp = todo & __ballot(key == lkey);
+    if (lane == leader) atomicAdd(&h[lkey], (unsigned)__popcll(grp));
+    todo &= ~grp;
+  }
+  if ((todo >> lane) & 1ull) atomicAdd(&h[key], 1u);
+}
+
 // ------------------------------------------------------------------------------------------------------------
 // scores + softmax
 // ------------------------------------------------------------------------------------------------------------
-constexpr int kScoreRows = 8;   // query blocks per workgroup
+constexpr int kScoreRows = 8;   // query blocks per workgroup (2 per wave of 256 threads)
+constexpr int kKeyChunk = 64;   // key blocks staged in LDS at a time
+constexpr int kKStride = kHeadDim + 4;   // padded LDS row of a pooled key (floats)
 constexpr int kHistBins = 4096; // top-12-bit bins (bits 30..19) of the prob bit patterns
 
 // pq: (nq, C) pooled queries; pk: pooled keys, logical key block j at row map.row(j)/128 of pk (C floats each);
@@ -85,8 +123,11 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
                                                              unsigned* __restrict__ hist, int q_slices) {
   extern __shared__ float sm[];
   __shared__ unsigned lhist[2][kHistBins];   // the (up to) two query slices of this workgroup's rows
-  float* qs = sm;                          // [kScoreRows][128]
-  float* ss = sm + kScoreRows * kHeadDim;  // [kScoreRows][nk]
+  float* qs = sm;                                      // [kScoreRows][128]
+  float* ks = qs + kScoreRows * kHeadDim;              // [kKeyChunk][kKStride]
+  float* ss = ks + kKeyChunk * kKStride;               // [kScoreRows][nk]
+  const int sw = min(s, nk);                           // local-window columns that key blocks 0..nk-1 use
+  uint8_t* lm = (uint8_t*)(ss + kScoreRows * nk);      // [kScoreRows][sw] local-window bytes of this group's rows
   const int h = blockIdx.y;
   const int i0 = blockIdx.x * kScoreRows;
   const int tid = threadIdx.x;
@@ -97,57 +138,110 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
     const int r = e / kHeadDim, d = e % kHeadDim;
     qs[e] = (i0 + r < nq) ? pq[(int64_t)(i0 + r) * C + h * kHeadDim + d] : 0.f;
   }
-  __syncthreads();
-  const float sqrt_d = sqrtf((float)kHeadDim);
-#pragma unroll 1
-  for (int j = tid; j < nk; j += blockDim.x) {
-    // keep the (loop-invariant) pooled-query reads inside the loop: hoisting 8 x 128 floats spills
-    asm volatile("" ::: "memory");
-    const float* krow = pk + (kmap.row(j) / kBlock) * C + h * kHeadDim;
-    float acc[kScoreRows];
-#pragma unroll
-    for (int r = 0; r < kScoreRows; ++r) acc[r] = 0.f;
-#pragma unroll 4
-    for (int d0 = 0; d0 < kHeadDim; d0 += 4) {
-      const f32x4 kv = *(const f32x4*)(krow + d0);
-#pragma unroll
-      for (int r = 0; r < kScoreRows; ++r) {
-        const f32x4 qv = *(const f32x4*)(qs + r * kHeadDim + d0);
-        acc[r] = fmaf(qv[0], kv[0], acc[r]);
-        acc[r] = fmaf(qv[1], kv[1], acc[r]);
-        acc[r] = fmaf(qv[2], kv[2], acc[r]);
-        acc[r] = fmaf(qv[3], kv[3], acc[r]);
-      }
-    }
-    const int ksp = j % s;
-#pragma unroll
-    for (int r = 0; r < kScoreRows; ++r) {
-      const int qsp = (i0 + r) % s;
-      ss[r * nk + j] = local[qsp * s + ksp] ? acc[r] / sqrt_d : -INFINITY;
-    }
+  for (int e = tid; e < kScoreRows * sw; e += blockDim.x) {
+    const int r = e / sw, c = e - r * sw;
+    lm[e] = local[((i0 + r) % s) * s + c];
   }
   __syncthreads();
-  const int wave = tid >> 6, lane = tid & 63, nwaves = blockDim.x >> 6;
+  const float sqrt_d = sqrtf((float)kHeadDim);
+  // Key blocks in chunks of 64: the chunk's pooled-key rows (64 x 512 B) are read with coalesced 16-byte loads
+  // (each wave load covers two whole rows) into padded LDS rows, the loads of the next two chunks in flight while
+  // the current one is multiplied. The products run on the matrix cores in fp32 (v_mfma_f32_16x16x4_f32): wave w takes keys
+  // 16w .. 16w + 15 of the chunk against the 8 query rows (padded to 16). Lane l holds A = Q[l % 16][32 (l / 16) + t]
+  // and B = K[16w + l % 16][32 (l / 16) + t] at step t (the reduction index of step t, lane group g is dim 32 g + t,
+  // so each lane reads 32 contiguous floats), and the 16 x 16 product lands as D[4 (l / 16) + v][l % 16], v < 4.
+  const int wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const float* kbase = pk + h * kHeadDim;
+  constexpr int kLoads = kKeyChunk * (kHeadDim / 4) / 256;   // 16-byte loads per thread per chunk
+  auto load_chunk = [&](f32x4 (&pre)[kLoads], int j0) {
+    const int nj = min(kKeyChunk, nk - j0);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int e = i * 256 + tid, jj = e >> 5, c4 = e & 31;
+      if (jj < nj) pre[i] = *(const f32x4*)(kbase + (kmap.row(j0 + jj) / kBlock) * C + 4 * c4);
+    }
+  };
+  float qa[32];   // this lane's A operands (query row li, dims 32 lg .. 32 lg + 31; rows >= 8 are zero)
+#pragma unroll
+  for (int t = 0; t < 32; t += 4) {
+    const f32x4 x = li < kScoreRows ? *(const f32x4*)(qs + li * kHeadDim + 32 * lg + t) : f32x4{0.f, 0.f, 0.f, 0.f};
+    qa[t] = x[0];
+    qa[t + 1] = x[1];
+    qa[t + 2] = x[2];
+    qa[t + 3] = x[3];
+  }
+  // one chunk: its rows to LDS, the loads of the chunk after next into the same registers, the products
+  auto chunk = [&](f32x4 (&pre)[kLoads], int j0) {
+    const int nj = min(kKeyChunk, nk - j0);
+    __syncthreads();   // the previous chunk's rows have been read
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int e = i * 256 + tid, jj = e >> 5, c4 = e & 31;
+      if (jj < nj) *(f32x4*)(ks + jj * kKStride + 4 * c4) = pre[i];
+    }
+    __syncthreads();
+    if (j0 + 2 * kKeyChunk < nk) load_chunk(pre, j0 + 2 * kKeyChunk);
+    if (16 * wave < nj) {   // wave-uniform; rows of keys past nj hold stale data and are not stored
+      const float* krow = ks + (16 * wave + li) * kKStride + 32 * lg;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 32; t += 4) {
+        const f32x4 kb = *(const f32x4*)(krow + t);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t], kb[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 1], kb[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 2], kb[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 3], kb[3], acc, 0, 0, 0);
+      }
+      const int jj = 16 * wave + li, j = j0 + jj;
+      if (lg < 2 && jj < nj) {   // rows 4 lg .. 4 lg + 3 < 8
+        const int ksp = j % s;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = 4 * lg + v;
+          ss[r * nk + j] = lm[r * sw + ksp] ? acc[v] / sqrt_d : -INFINITY;
+        }
+      }
+    }
+  };
+  f32x4 pa[kLoads], pb[kLoads];
+  load_chunk(pa, 0);
+  if (kKeyChunk < nk) load_chunk(pb, kKeyChunk);
+  for (int j0 = 0; j0 < nk; j0 += 2 * kKeyChunk) {
+    chunk(pa, j0);
+    if (j0 + kKeyChunk < nk) chunk(pb, j0 + kKeyChunk);
+  }
+  __syncthreads();
+  const int nwaves = blockDim.x >> 6;
   for (int r = wave; r < kScoreRows; r += nwaves) {
     if (i0 + r >= nq) break;
-    const float* srow = ss + r * nk;
+    float* srow = ss + r * nk;
     float mx = -INFINITY;
     for (int j = lane; j < nk; j += 64) mx = fmaxf(mx, srow[j]);
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     float sum = 0.f;
-    for (int j = lane; j < nk; j += 64) sum += expf(srow[j] - mx);
+    for (int j = lane; j < nk; j += 64) {
+      const float ex = expf(srow[j] - mx);
+      srow[j] = ex;   // each lane re-reads only its own entries below
+      sum += ex;
+    }
     for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
     float* prow = probs + ((int64_t)h * nq + i0 + r) * nk;
     const int dt = (i0 + r) / sq - t_first;   // 0 or 1 unless a slice holds fewer than kScoreRows blocks
     unsigned* grow = hist + ((int64_t)h * q_slices + (i0 + r) / sq) * kHistBins;
-    for (int j = lane; j < nk; j += 64) {
-      const float p = expf(srow[j] - mx) / sum;
-      prow[j] = p;
-      const unsigned u = __float_as_uint(p);
-      if (u != 0u) {
-        if (dt < 2) atomicAdd(&lhist[dt][u >> 19], 1u);
-        else atomicAdd(&grow[u >> 19], 1u);
+    for (int j0 = 0; j0 < nk; j0 += 64) {   // wave-uniform trip count (the histogram add needs every lane)
+      const int j = j0 + lane;
+      unsigned u = 0u;
+      if (j < nk) {
+        const float p = srow[j] / sum;
+        prow[j] = p;
+        u = __float_as_uint(p);
       }
+      // probs are in [0, 1], so u >> 19 < kHistBins; the mask only keeps a NaN (from NaN inputs) in bounds
+      const unsigned bin = (u >> 19) & (kHistBins - 1);
+      if (dt == 0) wave_hist_add(lhist[0], bin, u != 0u);   // dt is wave-uniform
+      else if (dt == 1) wave_hist_add(lhist[1], bin, u != 0u);
+      else wave_hist_add(grow, bin, u != 0u);
     }
   }
   __syncthreads();
@@ -160,11 +254,6 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
       if (c) atomicAdd(&g[bn], c);
     }
   }
-}
-
-__global__ void fill_zero_u32_kernel(unsigned* __restrict__ p, int64_t n) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e < n) p[e] = 0u;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -194,7 +283,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const floa
   __shared__ unsigned s_prefix, s_rank;
   __shared__ unsigned cand[kCand];
   __shared__ unsigned bins[kHistBins];
-  __shared__ unsigned s_ncand;
+  __shared__ unsigned s_ncand, s_fill;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row = blockIdx.x;                       // (head, query slice)
   const int h = row / q_slices, t = row % q_slices;
@@ -204,15 +293,29 @@ __global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const floa
   const int64_t n = (int64_t)sq * nk;
   const int64_t k = min<int64_t>(n - 1, topk);
 
+  // the whole row, when it fits, with every load in flight at once (thread tid holds elements i*1024 + tid); it
+  // serves both paths below. Padding never matches a bin or a prefix (bit 31 set).
+  const unsigned* hrow = hist12 + (int64_t)row * kHistBins;
+  unsigned hv[kHistBins / kTopkThreads];
+#pragma unroll
+  for (int i = 0; i < kHistBins / kTopkThreads; ++i) hv[i] = hrow[tid * (kHistBins / kTopkThreads) + i];
+  const bool in_regs = n <= (int64_t)kTopkThreads * kTopkRegs;
+  unsigned v[kTopkRegs];
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kTopkRegs; ++i) {
+      const int64_t e = (int64_t)i * kTopkThreads + tid;
+      v[i] = e < n ? bits[e] : 0xffffffffu;
+    }
+  }
+
   // ---- histogram-guided path ----
   {
-    const unsigned* hrow = hist12 + (int64_t)row * kHistBins;
     unsigned part = 0;
 #pragma unroll
     for (int i = 0; i < kHistBins / kTopkThreads; ++i) {
-      const unsigned c = hrow[tid * (kHistBins / kTopkThreads) + i];
-      bins[tid * (kHistBins / kTopkThreads) + i] = c;
-      part += c;
+      bins[tid * (kHistBins / kTopkThreads) + i] = hv[i];
+      part += hv[i];
     }
     // inclusive scan of the per-thread sums (1024 threads)
     unsigned incl = part;
@@ -247,18 +350,41 @@ __global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const floa
     const unsigned ncand = s_ncand;
     if (ncand <= (unsigned)kCand) {   // workgroup-uniform
       const unsigned bin = s_prefix >> 19;
-      if (tid == 0) s_ncand = 0;
-      __syncthreads();
-      // gather the elements of the bin (wave-aggregated slot reservation)
-      for (int64_t e0 = 0; e0 < n; e0 += kTopkThreads) {
-        const int64_t e = e0 + tid;
-        const unsigned u = e < n ? bits[e] : 0xffffffffu;
-        const bool in = (u >> 19) == bin;
-        const uint64_t m = __ballot(in);
-        unsigned slot = 0;
-        if (lane == 0 && m) slot = atomicAdd(&s_ncand, (unsigned)__popcll(m));
-        slot = __shfl(slot, 0);
-        if (in) cand[slot + __popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))))] = u;
+      if (in_regs) {
+        // gather the elements of the bin from registers: per-thread counts, a workgroup exclusive scan for the
+        // slots, then the writes (no atomics)
+        unsigned cnt = 0;
+#pragma unroll
+        for (int i = 0; i < kTopkRegs; ++i) cnt += (v[i] >> 19) == bin ? 1u : 0u;
+        unsigned inc = cnt;
+        for (int o = 1; o < 64; o <<= 1) {
+          const unsigned y = __shfl_up(inc, o);
+          if (lane >= o) inc += y;
+        }
+        __syncthreads();   // every thread has read tot[] of the bin search above
+        if (lane == 63) tot[wave] = inc;
+        __syncthreads();
+        unsigned slot = inc - cnt;
+        for (int w = 0; w < wave; ++w) slot += tot[w];
+#pragma unroll
+        for (int i = 0; i < kTopkRegs; ++i)
+          if ((v[i] >> 19) == bin && slot < (unsigned)kCand) cand[slot++] = v[i];
+      } else {
+        // (a counter of its own: s_ncand may still be read by waves that have not reached this point)
+        if (tid == 0) s_fill = 0;
+        __syncthreads();
+        // gather the elements of the bin from memory (wave-aggregated slot reservation)
+        for (int64_t e0 = 0; e0 < n; e0 += kTopkThreads) {
+          const int64_t e = e0 + tid;
+          const unsigned u = e < n ? bits[e] : 0xffffffffu;
+          const bool in = (u >> 19) == bin;
+          const uint64_t m = __ballot(in);
+          unsigned slot = 0;
+          if (lane == 0 && m) slot = atomicAdd(&s_fill, (unsigned)__popcll(m));
+          slot = __shfl(slot, 0);
+          const unsigned at = slot + __popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+          if (in && at < (unsigned)kCand) cand[at] = u;
+        }
       }
       __syncthreads();
       unsigned prefix = s_prefix, rk = s_rank;
@@ -270,9 +396,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const floa
         const unsigned dmask = dmasks[pass];
         for (int e = tid; e < (kTopkThreads / 64) * 256; e += kTopkThreads) (&hist[0][0])[e] = 0;
         __syncthreads();
-        for (int e = tid; e < (int)ncand; e += kTopkThreads) {
-          const unsigned u = cand[e];
-          if ((u & pmask) == prefix) atomicAdd(&hist[wave][(u >> shift) & dmask], 1u);
+        for (int e0 = 0; e0 < (int)ncand; e0 += kTopkThreads) {   // uniform trip count for wave_hist_add
+          const int e = e0 + tid;
+          const unsigned u = e < (int)ncand ? cand[e] : 0xffffffffu;
+          wave_hist_add(hist[wave], (u >> shift) & dmask, (u & pmask) == prefix);
         }
         __syncthreads();
         if (tid < 256) {
@@ -315,15 +442,6 @@ __global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const floa
   }
 
   // ---- full-row radix select (the bin is too large for LDS) ----
-  const bool in_regs = n <= (int64_t)kTopkThreads * kTopkRegs;
-  unsigned v[kTopkRegs];
-  if (in_regs) {
-#pragma unroll
-    for (int i = 0; i < kTopkRegs; ++i) {
-      const int64_t e = (int64_t)i * kTopkThreads + tid;
-      v[i] = e < n ? bits[e] : 0xffffffffu;   // padding never matches a prefix (bit 31 set)
-    }
-  }
   unsigned rank = (unsigned)(n - 1 - k);            // ascending rank of the (k+1)-th largest
   unsigned prefix = 0, pmask = 0x80000000u;
   if (tid == 0) {
@@ -341,7 +459,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const floa
       const bool match = (u & pmask) == prefix;
       const bool z = match && u == 0u;
       zeros += __popcll(__ballot(z));
-      if (match && !z) atomicAdd(&hist[wave][(u >> shift) & dmask], 1u);
+      wave_hist_add(hist[wave], (u >> shift) & dmask, match && !z);
     };
     if (in_regs) {
 #pragma unroll
@@ -435,45 +553,44 @@ __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict_
 // ------------------------------------------------------------------------------------------------------------
 // launch
 // ------------------------------------------------------------------------------------------------------------
-int launch_pool_finish(const float* partial, int nb, int C, int64_t L, int dst_slot0, int capacity,
-                       int slice_blocks, float* out, hipStream_t stream);   // kv_ring.hip
-
-// the per-run block sums of x (L tokens): partial[(b * kPoolParts + part) * C + c], (ceil(L/128) * kPoolParts, C)
-int launch_pool_parts(int dtype, const void* x, int64_t L, int C, float* partial, hipStream_t stream) {
-  const int nb = (int)ceil_div(L, kBlock);
+// the per-run block sums of n (1..3) sources in one launch; each source's nb is set here from its L
+int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream) {
+  PoolSrc s[3] = {};
+  int nb = 0;
+  for (int i = 0; i < n && i < 3; ++i) {
+    s[i] = src[i];
+    s[i].nb = (int)ceil_div(std::max<int64_t>(0, s[i].L), kBlock);
+    src[i].nb = s[i].nb;
+    nb += s[i].nb;
+  }
   if (nb <= 0) return FVSR_OK;
   const int vn = dtype == FVSR_DTYPE_BF16 ? 8 : 4;
   const int nvec = C / vn;
   const int threads = std::min(1024, ((nvec + 63) / 64) * 64);
   const dim3 grid(nb, kPoolParts);
   if (dtype == FVSR_DTYPE_BF16)
-    hipLaunchKernelGGL(pool_part_kernel<bf16>, grid, dim3(threads), 0, stream, (const bf16*)x, L, C, partial);
+    hipLaunchKernelGGL(pool_part_kernel<bf16>, grid, dim3(threads), 0, stream, s[0], s[1], s[2], C);
   else
-    hipLaunchKernelGGL(pool_part_kernel<float>, grid, dim3(threads), 0, stream, (const float*)x, L, C, partial);
+    hipLaunchKernelGGL(pool_part_kernel<float>, grid, dim3(threads), 0, stream, s[0], s[1], s[2], C);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }
 
-// block means of x: partial (ceil(L/128) * kPoolParts, C) fp32 scratch
-int launch_pool(int dtype, const void* x, int64_t L, int C, float* out, float* partial, hipStream_t stream) {
-  const int nb = (int)ceil_div(L, kBlock);
-  if (nb <= 0) return FVSR_OK;
-  const int rc = launch_pool_parts(dtype, x, L, C, partial, stream);
-  if (rc) return rc;
-  return launch_pool_finish(partial, nb, C, L, 0, 1, 1 << 30, out, stream);
+size_t scores_smem_bytes(int nk, int s) {
+  return sizeof(float) * ((size_t)kScoreRows * (kHeadDim + nk) + (size_t)kKeyChunk * kKStride) +
+         (size_t)kScoreRows * std::min(s, nk);
 }
 
-size_t scores_smem_bytes(int nk) { return sizeof(float) * (size_t)kScoreRows * (kHeadDim + nk); }
-
-// hist: (heads * q_slices * kHistBins) u32 workspace, zeroed here before the scores
+// hist: (heads * q_slices * kHistBins) u32 workspace, zeroed by the caller before the launch (pool_finish_kernel
+// clears it together with the pooled queries)
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
                           const uint8_t* local, float* probs, unsigned* hist, int q_slices, hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;
-  const int64_t nh = (int64_t)heads * q_slices * kHistBins;
-  hipLaunchKernelGGL(fill_zero_u32_kernel, dim3((unsigned)ceil_div(nh, 256)), dim3(256), 0, stream, hist, nh);
-  FVSR_HIP_CHECK(hipGetLastError());
   dim3 grid((nq + kScoreRows - 1) / kScoreRows, heads);
-  hipLaunchKernelGGL(scores_softmax_kernel, grid, dim3(256), scores_smem_bytes(nk), stream, pq, pk, kmap, C, nq,
+  const size_t smem = scores_smem_bytes(nk, s);
+  if (smem + sizeof(unsigned) * 2 * kHistBins > 160 * 1024)
+    return set_error(FVSR_ERR_UNSUPPORTED, "scores stage: too many key blocks for LDS");
+  hipLaunchKernelGGL(scores_softmax_kernel, grid, dim3(256), smem, stream, pq, pk, kmap, C, nq,
                      nk, s, local, probs, hist, q_slices);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
