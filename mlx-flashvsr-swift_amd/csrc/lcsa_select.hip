@@ -122,9 +122,11 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
                                                              float* __restrict__ probs,
                                                              unsigned* __restrict__ hist, int q_slices) {
   extern __shared__ float sm[];
-  __shared__ unsigned lhist[2][kHistBins];   // the (up to) two query slices of this workgroup's rows
   float* qs = sm;                                      // [kScoreRows][128]
   float* ks = qs + kScoreRows * kHeadDim;              // [kKeyChunk][kKStride]
+  // the workgroup histograms of the (up to) two query slices of its rows, [2][kHistBins]: they reuse the key chunk
+  // staging once the scores are done (keeping the LDS of a workgroup small enough for 3 per CU)
+  unsigned* lhist = (unsigned*)ks;
   float* ss = ks + kKeyChunk * kKStride;               // [kScoreRows][nk]
   const int sw = min(s, nk);                           // local-window columns that key blocks 0..nk-1 use
   uint8_t* lm = (uint8_t*)(ss + kScoreRows * nk);      // [kScoreRows][sw] local-window bytes of this group's rows
@@ -133,7 +135,6 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
   const int tid = threadIdx.x;
   const int sq = nq / q_slices;                 // query blocks per slice
   const int t_first = i0 / sq;
-  for (int e = tid; e < 2 * kHistBins; e += blockDim.x) (&lhist[0][0])[e] = 0;
   for (int e = tid; e < kScoreRows * kHeadDim; e += blockDim.x) {
     const int r = e / kHeadDim, d = e % kHeadDim;
     qs[e] = (i0 + r < nq) ? pq[(int64_t)(i0 + r) * C + h * kHeadDim + d] : 0.f;
@@ -212,6 +213,8 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
     if (j0 + kKeyChunk < nk) chunk(pb, j0 + kKeyChunk);
   }
   __syncthreads();
+  for (int e = tid; e < 2 * kHistBins; e += blockDim.x) lhist[e] = 0u;
+  __syncthreads();
   const int nwaves = blockDim.x >> 6;
   for (int r = wave; r < kScoreRows; r += nwaves) {
     if (i0 + r >= nq) break;
@@ -239,8 +242,8 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
       }
       // probs are in [0, 1], so u >> 19 < kHistBins; the mask only keeps a NaN (from NaN inputs) in bounds
       const unsigned bin = (u >> 19) & (kHistBins - 1);
-      if (dt == 0) wave_hist_add(lhist[0], bin, u != 0u);   // dt is wave-uniform
-      else if (dt == 1) wave_hist_add(lhist[1], bin, u != 0u);
+      if (dt == 0) wave_hist_add(lhist, bin, u != 0u);   // dt is wave-uniform
+      else if (dt == 1) wave_hist_add(lhist + kHistBins, bin, u != 0u);
       else wave_hist_add(grow, bin, u != 0u);
     }
   }
@@ -250,7 +253,7 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
   for (int dt = 0; dt < 2 && t_first + dt <= t_last; ++dt) {
     unsigned* g = hist + ((int64_t)h * q_slices + t_first + dt) * kHistBins;
     for (int bn = tid; bn < kHistBins; bn += blockDim.x) {
-      const unsigned c = lhist[dt][bn];
+      const unsigned c = lhist[dt * kHistBins + bn];
       if (c) atomicAdd(&g[bn], c);
     }
   }
@@ -577,6 +580,7 @@ int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream)
 }
 
 size_t scores_smem_bytes(int nk, int s) {
+  static_assert(kKeyChunk * kKStride * sizeof(float) >= 2 * kHistBins * sizeof(unsigned), "histograms alias ks");
   return sizeof(float) * ((size_t)kScoreRows * (kHeadDim + nk) + (size_t)kKeyChunk * kKStride) +
          (size_t)kScoreRows * std::min(s, nk);
 }
@@ -588,7 +592,7 @@ int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int hea
   if (nq <= 0 || nk <= 0) return FVSR_OK;
   dim3 grid((nq + kScoreRows - 1) / kScoreRows, heads);
   const size_t smem = scores_smem_bytes(nk, s);
-  if (smem + sizeof(unsigned) * 2 * kHistBins > 160 * 1024)
+  if (smem > 160 * 1024)
     return set_error(FVSR_ERR_UNSUPPORTED, "scores stage: too many key blocks for LDS");
   hipLaunchKernelGGL(scores_softmax_kernel, grid, dim3(256), smem, stream, pq, pk, kmap, C, nq,
                      nk, s, local, probs, hist, q_slices);
