@@ -50,6 +50,10 @@ def parse_args():
                          "(normQ/normK + RoPE + window partition + ring append fused, output window-reversed)")
     ap.add_argument("--epilogue", action="store_true",
                     help="time the fused QKV epilogue into the KV ring on one 1920x1152 streaming chunk (HBM-bound)")
+    ap.add_argument("--block", action="store_true",
+                    help="time one whole DiT block (blockForward: norms, modulation, q/k/v/o, LCSA layer call, "
+                         "cross-attention over 512 context tokens, FFN 1536->8960->1536) on a steady 1920x1152 "
+                         "streaming chunk; prints its own JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain copy of known size (the window-partition kernel over 16x72x120 bf16 "
                          "tokens of 1536 channels: 424.7 MB read + 424.7 MB written per launch), the reference "
@@ -289,6 +293,77 @@ def epilogue_bench(args):
         "algorithmic_bytes": nbytes}), flush=True)
 
 
+def block_bench(args):
+    """One streaming `blockForward` (DiT.swift:491-551) of the Wan2.1-1.3B-shaped DiT (dim 1536, 12 heads, FFN 8960,
+    512 context tokens) on a steady 1920x1152 chunk: 2 latent frames = 17280 tokens, KV window of 3 slices + the new
+    one (135 x 540 key blocks, top-k 16199, local range 11). Random-init weights (no checkpoint), synthetic tokens;
+    the ring is filled by a first chunk of 3 slices before timing. FLOPs per call: GEMMs 17280 x (12 C^2 + 4 C F)
+    = 1.4405 TFLOP, cross-attention 4 x 17280 x 512 x C = 0.0544 TFLOP, LCSA kept blocks 12 x 16199 x 128^3 x 4 =
+    1.6306 TFLOP (top-k keeps exactly 16199 pairs per (head, slice) without ties)."""
+    import torch
+
+    import fvsr_lcsa
+    from fvsr_lcsa import synth
+
+    dev = torch.device("cuda:0")
+    H, bh, bw, F, n_ctx = 12, 9, 15, 8960, 512
+    C, s = H * 128, bh * bw
+    lat_h, lat_w = 8 * bh, 8 * bw
+    local = fvsr_lcsa.local_block_mask(bh, bw, 11)
+    topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(shape, generator=gen, device=dev) * scale).to(torch.bfloat16)
+
+    W = {"modulation": rnd(6, C, scale=0.1)}
+    for p in ("q", "k", "v", "o", "cross_q", "cross_k", "cross_v", "cross_o"):
+        W[p + "_weight"] = rnd(C, C, scale=C ** -0.5)
+        W[p + "_bias"] = rnd(C, scale=0.05)
+    for p in ("norm_q", "norm_k", "cross_norm_q", "cross_norm_k", "norm3"):
+        W[p + "_weight"] = (1 + 0.1 * torch.randn(C, generator=gen, device=dev)).to(torch.bfloat16)
+    W["norm3_bias"] = rnd(C, scale=0.05)
+    W["ffn1_weight"], W["ffn1_bias"] = rnd(F, C, scale=C ** -0.5), rnd(F, scale=0.05)
+    W["ffn2_weight"], W["ffn2_bias"] = rnd(C, F, scale=F ** -0.5), rnd(C, scale=0.05)
+    blk = fvsr_lcsa.DiTBlock(W, H)
+    blk.set_context(rnd(n_ctx, C))
+    t_mod = rnd(6, C, scale=0.1)
+    ring = fvsr_lcsa.KVRing(1, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    x0 = rnd(6 * lat_h * lat_w, C)
+    blk.forward(ring, 0, x0, t_mod, 3, 0, local, topk)   # chunk 0: 3 slices fill the window
+    L = 2 * lat_h * lat_w
+    x = rnd(L, C)
+    t0 = 6
+    for _ in range(max(2, args.warmup)):
+        blk.forward(ring, 0, x, t_mod, 1, t0, local, topk)
+    torch.cuda.synchronize()
+    n = max(5, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        blk.forward(ring, 0, x, t_mod, 1, t0, local, topk)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    if not torch.isfinite(x.float()).all():
+        raise RuntimeError("DiT block produced non-finite tokens")
+    gemm = 2.0 * L * (6 * C * C + 2 * C * F)   # q, k, v, o, cross q, cross o; FFN up and down
+    cross = 4.0 * L * n_ctx * C
+    lcsa = 4.0 * 128 ** 3 * H * topk
+    total = gemm + cross + lcsa
+    print(json.dumps({
+        "metric": "DiT block (blockForward) per steady streaming chunk, 1920x1152",
+        "value": round(ms, 4), "unit": "ms per block call", "higher_is_better": False, "n_gpus": 1, "dtype": "bf16",
+        "data": "synthetic tokens, random-init weights (no checkpoint)",
+        "config": {"workload": "dit_block_1920x1152_bf16", "tokens": L, "dim": C, "heads": H, "ffn_dim": F,
+                   "context_tokens": n_ctx, "key_blocks": 4 * s, "topk": topk, "local_range": 11},
+        "tflop_per_call": {"gemm": round(gemm / 1e12, 4), "cross_attention": round(cross / 1e12, 4),
+                           "lcsa_kept": round(lcsa / 1e12, 4)},
+        "effective_tflops": round(total / (ms * 1e-3) / 1e12, 1),
+        "per_chunk_ms_30_blocks": round(30 * ms, 2),
+        "steps": n}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -309,6 +384,9 @@ def main():
         return
     if args.epilogue:
         epilogue_bench(args)
+        return
+    if args.block:
+        block_bench(args)
         return
     dev = torch.device("cuda:0")
     wl = synth.WORKLOADS[args.workload]

@@ -184,6 +184,46 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const void
                         const float* rope_tables, const uint8_t* local_dev, int topk, int mode, void* q_work, void* o,
                         float* mask_out, float* probs_out, void* stream);
 
+/* ---- (f3) the dense parts of the DiT block ------------------------------------------------------------------ */
+/* `Linear` (MLX, DiT.swift:319-321,371): y = x W^T + b on hipBLASLt, bf16 in/out, fp32 accumulate. x: (rows,
+ * in_features); weight: (out_features, in_features) row-major; bias: (out_features) or NULL; gelu != 0 applies the
+ * tanh-form GELU of `GELU(approximation: .tanh)` (DiT.swift:371) to the fp32 result before the bf16 store. Feature
+ * counts must be multiples of 8. The first call on a context creates its hipBLASLt handle and 64 MB GEMM workspace. */
+int fvsr_linear(fvsr_ctx* ctx, const void* x, int64_t rows, int in_features, const void* weight, int out_features,
+                const void* bias, int gelu, void* y, void* stream);
+
+/* Weights of one `DiTBlock` (DiT.swift:363-375), bf16 device pointers, Linear weights (out, in) row-major; any
+ * bias may be NULL. C = heads * 128. */
+typedef struct fvsr_dit_block_weights {
+  const void* modulation;                                      /* (6, C) */
+  const void *q_weight, *q_bias, *k_weight, *k_bias;           /* self-attention (C, C), (C) */
+  const void *v_weight, *v_bias, *o_weight, *o_bias;
+  const void *norm_q_weight, *norm_k_weight;                   /* WanRMSNorm weights (C) */
+  const void *cross_q_weight, *cross_q_bias, *cross_k_weight, *cross_k_bias;   /* cross-attention */
+  const void *cross_v_weight, *cross_v_bias, *cross_o_weight, *cross_o_bias;
+  const void *cross_norm_q_weight, *cross_norm_k_weight;
+  const void *cross_k, *cross_v;                               /* (ctx_len, C) cached context K/V */
+  int ctx_len;
+  const void *norm3_weight, *norm3_bias;                       /* LayerNorm(affine) (C) */
+  const void *ffn1_weight, *ffn1_bias, *ffn2_weight, *ffn2_bias; /* (F, C), (F), (C, F), (C) */
+  int ffn_dim;                                                 /* F, a multiple of 8 */
+} fvsr_dit_block_weights;
+
+/* `CrossAttention.initCache` (DiT.swift:346-350): k_out = normK(k(context)), v_out = v(context), context (ctx_len, C)
+ * bf16 (the text-embedded prompt); the results go to cross_k / cross_v of the weights. Once per context. */
+int fvsr_dit_cross_kv(fvsr_ctx* ctx, const fvsr_dit_block_weights* w, int heads, const void* context, int ctx_len,
+                      float eps, void* k_out, void* v_out, void* stream);
+
+/* One streaming `blockForward` (DiT.swift:491-551) of block `layer`: x (L, C) bf16 in natural (f, h, w) token
+ * order, L = 2*n_new_slices * 8bh * 8bw, updated in place. t_mod: (6, C) bf16 time modulation. norm1 / norm2 /
+ * norm3 (eps), modulation, the q/k/v projections, fvsr_lcsa_layer_qkv on `ring` (selection + attention + cache
+ * append/evict; topk, mode, local window and RoPE as there), the o projection and gated residual, the
+ * cross-attention over w->cross_k / cross_v, and the FFN with its gated residual. Activations live in a block
+ * workspace of the context (about (8 * C + F) * L * 2 bytes), grown on the first call of a size. */
+int fvsr_dit_block(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const fvsr_dit_block_weights* w, const void* t_mod,
+                   void* x, int n_new_slices, int t0, float eps, const float* rope_tables, const uint8_t* local_dev,
+                   int topk, int mode, void* stream);
+
 /* ---- (a1) window layout ------------------------------------------------------------------------------------ */
 /* Replace `windowPartition` / `windowReverse` (DiT.swift:113-126): (f*h*w, C) natural <-> window order. */
 int fvsr_window_partition(int dtype, const void* x, void* out, int f, int h, int w, int channels, void* stream);

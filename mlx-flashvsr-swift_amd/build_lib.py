@@ -18,7 +18,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libfvsr_lcsa.so")
 PROBE = os.path.join(LIB_DIR, "fvsr_probe_attn")
 
-SOURCES = ["api.hip", "lcsa_attn.hip", "lcsa_select.hip", "kv_ring.hip", "qkv_epilogue.hip"]
+SOURCES = ["api.hip", "lcsa_attn.hip", "lcsa_select.hip", "kv_ring.hip", "qkv_epilogue.hip", "dit_block.hip"]
 # Packed-FP32 VALU forms are disabled: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32 from float code.
 # MFMA builtins get the VGPR form (results in VGPRs, where the VALU reads them without v_accvgpr_read); the attention
 # kernels write the one AGPR-accumulating MFMA as inline assembly.
@@ -49,7 +49,8 @@ def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     hipcc = _hipcc()
     tmp = LIB + ".tmp"
-    _run([hipcc, *HIP_FLAGS, "-shared", *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp], verbose)
+    # hipBLASLt for the DiT block's GEMMs (fvsr_linear / fvsr_dit_block)
+    _run([hipcc, *HIP_FLAGS, "-shared", *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp, "-lhipblaslt"], verbose)
     os.replace(tmp, LIB)
     probe_src = os.path.join(HOST, "probe_attn.cpp")
     if os.path.exists(probe_src):

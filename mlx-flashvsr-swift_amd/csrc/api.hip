@@ -38,6 +38,15 @@ int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, 
 int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream);
 int launch_pool_finish(const PoolDst* dst, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream);
 int rope_table_floats();
+int blas_create(int device, void** out);
+void blas_destroy(void* p);
+int linear_bf16(void* state, const void* x, int64_t L, int K, const void* w, int N, const void* bias, int epilogue,
+                void* y, hipStream_t stream);
+int launch_modulation(const void* m, const void* t, void* out, int C, hipStream_t stream);
+int launch_residual_norm(void* x, const void* y, const void* gate, int64_t L, int C, float eps, const void* w,
+                         const void* bias, const void* scale, const void* shift, void* out, hipStream_t stream);
+int launch_rms_norm(const void* x, int64_t L, int C, float eps, const void* w, void* out, hipStream_t stream);
+int launch_full_lists(int rows, int nkc, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
 void rope_tables_host(double theta, float* out);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
                        int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
@@ -85,6 +94,9 @@ struct fvsr_ctx {
   int device = 0;
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  void* block_ws = nullptr;   // DiT block activations (separate from ws, which the layer call may grow)
+  size_t block_ws_bytes = 0;
+  void* blas = nullptr;       // hipBLASLt handle, GEMM workspace and algorithm cache (dit_block.hip)
 };
 
 struct fvsr_kv_ring {
@@ -161,10 +173,10 @@ int fvsr_ctx_create(int device, fvsr_ctx** out) {
 
 int fvsr_ctx_destroy(fvsr_ctx* ctx) {
   if (!ctx) return FVSR_OK;
-  if (ctx->ws) {
-    (void)hipSetDevice(ctx->device);
-    (void)hipFree(ctx->ws);
-  }
+  (void)hipSetDevice(ctx->device);
+  if (ctx->ws) (void)hipFree(ctx->ws);
+  if (ctx->block_ws) (void)hipFree(ctx->block_ws);
+  blas_destroy(ctx->blas);
   delete ctx;
   return FVSR_OK;
 }
@@ -727,6 +739,160 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q
   rc = attention_ring_impl(ctx, r, layer, q_work, lq, kidx, kcnt, nk, sel, use == FVSR_ATTN_DENSE, o, st, true);
   if (rc) return rc;
   return fvsr_kv_ring_evict(r, layer);
+}
+
+
+// ---------------------------------------------------------------------------------------------------------------
+// (f3) the dense parts of the DiT block
+// ---------------------------------------------------------------------------------------------------------------
+}  // extern "C"
+
+static int ensure_blas(fvsr_ctx* ctx) {
+  if (ctx->blas) return FVSR_OK;
+  return blas_create(ctx->device, &ctx->blas);
+}
+
+static int ensure_block_ws(fvsr_ctx* ctx, size_t bytes) {
+  if (ctx->block_ws_bytes >= bytes) return FVSR_OK;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if (ctx->block_ws) FVSR_HIP_CHECK(hipFree(ctx->block_ws));
+  ctx->block_ws = nullptr;
+  ctx->block_ws_bytes = 0;
+  if (hipMalloc(&ctx->block_ws, bytes) != hipSuccess) {
+    ctx->block_ws = nullptr;
+    return set_error(FVSR_ERR_OUT_OF_MEMORY, "block workspace allocation of " + std::to_string(bytes) + " bytes failed");
+  }
+  ctx->block_ws_bytes = bytes;
+  return FVSR_OK;
+}
+
+// activations of one block call: L tokens of C channels, FFN width F, cross-attention lists for nq query blocks
+struct BlockCarve {
+  size_t mod, in, q, k, v, qw, attn, tmp, ffn, kidx, kcnt, total;
+};
+static BlockCarve block_carve(int64_t L, int C, int F, int64_t nq, int nkc) {
+  BlockCarve c;
+  size_t off = 0;
+  const size_t tok = align256((size_t)L * C * 2);
+  c.mod = off; off += align256((size_t)6 * C * 2);
+  c.in = off; off += tok;
+  c.q = off; off += tok;
+  c.k = off; off += tok;
+  c.v = off; off += tok;
+  c.qw = off; off += tok;
+  c.attn = off; off += tok;
+  c.tmp = off; off += tok;
+  c.ffn = off; off += align256((size_t)L * F * 2);
+  c.kidx = off; off += align256((size_t)nq * nkc * 4);
+  c.kcnt = off; off += align256((size_t)nq * 4);
+  c.total = off;
+  return c;
+}
+
+static int check_block_weights(const fvsr_dit_block_weights* w, bool need_self, bool need_cross_kv) {
+  FVSR_REQUIRE(w != nullptr, FVSR_ERR_INVALID_ARG, "weights is NULL");
+  if (need_self)
+    FVSR_REQUIRE(w->modulation && w->q_weight && w->k_weight && w->v_weight && w->o_weight && w->norm_q_weight &&
+                     w->norm_k_weight && w->cross_q_weight && w->cross_o_weight && w->cross_norm_q_weight &&
+                     w->norm3_weight && w->ffn1_weight && w->ffn2_weight && w->cross_k && w->cross_v,
+                 FVSR_ERR_INVALID_ARG, "a weight pointer of the block is NULL (biases may be NULL)");
+  if (need_cross_kv)
+    FVSR_REQUIRE(w->cross_k_weight && w->cross_v_weight && w->cross_norm_k_weight, FVSR_ERR_INVALID_ARG,
+                 "cross k / v / norm_k weights must be non-NULL");
+  FVSR_REQUIRE(w->ffn_dim > 0 && w->ffn_dim % 8 == 0, FVSR_ERR_INVALID_ARG, "ffn_dim must be a positive multiple of 8");
+  return FVSR_OK;
+}
+
+extern "C" {
+
+int fvsr_linear(fvsr_ctx* ctx, const void* x, int64_t rows, int in_features, const void* weight, int out_features,
+                const void* bias, int gelu, void* y, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  FVSR_REQUIRE(x && weight && y, FVSR_ERR_INVALID_ARG, "x, weight and y must be non-NULL");
+  FVSR_REQUIRE(rows >= 0 && in_features > 0 && out_features > 0, FVSR_ERR_INVALID_ARG, "bad GEMM shape");
+  FVSR_REQUIRE(in_features % 8 == 0 && out_features % 8 == 0, FVSR_ERR_UNSUPPORTED,
+               "in_features and out_features must be multiples of 8");
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  int rc = ensure_blas(ctx);
+  if (rc) return rc;
+  return linear_bf16(ctx->blas, x, rows, in_features, weight, out_features, bias, gelu ? 1 : 0, y,
+                     (hipStream_t)stream);
+}
+
+int fvsr_dit_cross_kv(fvsr_ctx* ctx, const fvsr_dit_block_weights* w, int heads, const void* context, int ctx_len,
+                      float eps, void* k_out, void* v_out, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_block_weights(w, false, true);
+  if (rc) return rc;
+  if ((rc = check_heads(heads))) return rc;
+  FVSR_REQUIRE(context && k_out && v_out && ctx_len > 0, FVSR_ERR_INVALID_ARG, "context, k_out, v_out, ctx_len");
+  const int C = heads * kHeadDim;
+  hipStream_t st = (hipStream_t)stream;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if ((rc = ensure_blas(ctx))) return rc;
+  // k = normK(k(ctx)), v = v(ctx) (CrossAttention.initCache, DiT.swift:346-350); k_out doubles as the scratch
+  if ((rc = linear_bf16(ctx->blas, context, ctx_len, C, w->cross_k_weight, C, w->cross_k_bias, 0, k_out, st))) return rc;
+  if ((rc = launch_rms_norm(k_out, ctx_len, C, eps, w->cross_norm_k_weight, k_out, st))) return rc;
+  return linear_bf16(ctx->blas, context, ctx_len, C, w->cross_v_weight, C, w->cross_v_bias, 0, v_out, st);
+}
+
+int fvsr_dit_block(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const fvsr_dit_block_weights* w, const void* t_mod,
+                   void* x, int n_new_slices, int t0, float eps, const float* rope_tables, const uint8_t* local_dev,
+                   int topk, int mode, void* stream) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_layer(r, layer);
+  if (rc) return rc;
+  if ((rc = check_block_weights(w, true, false))) return rc;
+  FVSR_REQUIRE(r->dtype == FVSR_DTYPE_BF16, FVSR_ERR_UNSUPPORTED, "the DiT block runs in bf16");
+  FVSR_REQUIRE(t_mod && x && rope_tables && local_dev, FVSR_ERR_INVALID_ARG, "t_mod, x, rope_tables, local");
+  FVSR_REQUIRE(n_new_slices > 0 && w->ctx_len > 0, FVSR_ERR_INVALID_ARG, "n_new_slices and ctx_len must be > 0");
+  const int C = r->C, F = w->ffn_dim;
+  const int64_t L = (int64_t)n_new_slices * r->s * kBlock;   // 2 * n_new_slices frames of 8bh x 8bw tokens
+  const int64_t nq = ceil_div(L, kBlock);
+  const int nkc = (int)ceil_div(w->ctx_len, kBlock);
+  hipStream_t st = (hipStream_t)stream;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if ((rc = ensure_blas(ctx))) return rc;
+  const BlockCarve bc = block_carve(L, C, F, (int64_t)r->heads * nq, nkc);
+  if ((rc = ensure_block_ws(ctx, bc.total))) return rc;
+  char* ws = (char*)ctx->block_ws;
+  bf16* mod = (bf16*)(ws + bc.mod);
+  void *in = ws + bc.in, *q = ws + bc.q, *k = ws + bc.k, *v = ws + bc.v, *qw = ws + bc.qw, *attn = ws + bc.attn;
+  void *tmp = ws + bc.tmp, *ffn = ws + bc.ffn;
+  int32_t* kidx = (int32_t*)(ws + bc.kidx);
+  int32_t* kcnt = (int32_t*)(ws + bc.kcnt);
+  auto row = [&](int i) -> const void* { return mod + (size_t)i * C; };   // shift/scale/gate MSA, shift/scale/gate MLP
+  void* blas = ctx->blas;
+  // mod = modulation + t_mod; inX = norm1(x) * (1 + scaleMSA) + shiftMSA (DiT.swift:495-498)
+  if ((rc = launch_modulation(w->modulation, t_mod, mod, C, st))) return rc;
+  if ((rc = launch_residual_norm(x, nullptr, nullptr, L, C, eps, nullptr, nullptr, row(1), row(0), in, st))) return rc;
+  // self-attention: projections, the LCSA layer call (norm + RoPE + partition + ring + select + attend + evict,
+  // output in natural order), o projection (DiT.swift:500-539)
+  if ((rc = linear_bf16(blas, in, L, C, w->q_weight, C, w->q_bias, 0, q, st))) return rc;
+  if ((rc = linear_bf16(blas, in, L, C, w->k_weight, C, w->k_bias, 0, k, st))) return rc;
+  if ((rc = linear_bf16(blas, in, L, C, w->v_weight, C, w->v_bias, 0, v, st))) return rc;
+  if ((rc = fvsr_lcsa_layer_qkv(ctx, r, layer, q, k, v, n_new_slices, t0, w->norm_q_weight, w->norm_k_weight, eps,
+                                rope_tables, local_dev, topk, mode, qw, attn, nullptr, nullptr, stream)))
+    return rc;
+  if ((rc = linear_bf16(blas, attn, L, C, w->o_weight, C, w->o_bias, 0, tmp, st))) return rc;
+  // x = x + gateMSA * o; caIn = norm3(x) (affine) (DiT.swift:541-542)
+  if ((rc = launch_residual_norm(x, tmp, row(2), L, C, eps, w->norm3_weight, w->norm3_bias, nullptr, nullptr, in, st)))
+    return rc;
+  // cross-attention: q = normQ(q(caIn)); SDPA over the cached context K/V (every context block listed, scale
+  // 1/sqrt(128)); o projection (DiT.swift:352-361)
+  if ((rc = linear_bf16(blas, in, L, C, w->cross_q_weight, C, w->cross_q_bias, 0, q, st))) return rc;
+  if ((rc = launch_rms_norm(q, L, C, eps, w->cross_norm_q_weight, q, st))) return rc;
+  if ((rc = launch_full_lists((int)(r->heads * nq), nkc, kidx, kcnt, st))) return rc;
+  if ((rc = fvsr_lcsa_attention(ctx, FVSR_DTYPE_BF16, q, L, w->cross_k, w->cross_v, w->ctx_len, r->heads, kidx, kcnt,
+                                nkc, attn, stream)))
+    return rc;
+  if ((rc = linear_bf16(blas, attn, L, C, w->cross_o_weight, C, w->cross_o_bias, 0, tmp, st))) return rc;
+  // x = x + caOut; inF = norm2(x) * (1 + scaleMLP) + shiftMLP (DiT.swift:545-546)
+  if ((rc = launch_residual_norm(x, tmp, nullptr, L, C, eps, nullptr, nullptr, row(4), row(3), in, st))) return rc;
+  // FFN: Linear(C, F) + GELU(tanh) fused, Linear(F, C); x = x + gateMLP * ffn (DiT.swift:547)
+  if ((rc = linear_bf16(blas, in, L, C, w->ffn1_weight, F, w->ffn1_bias, 1, ffn, st))) return rc;
+  if ((rc = linear_bf16(blas, ffn, L, F, w->ffn2_weight, C, w->ffn2_bias, 0, tmp, st))) return rc;
+  return launch_residual_norm(x, tmp, row(5), L, C, eps, nullptr, nullptr, nullptr, nullptr, nullptr, st);
 }
 
 }  // extern "C"

@@ -11,6 +11,8 @@ Names mirror the reference's call surface (xocialize/mlx-flashvsr-swift):
   window_partition / reverse  windowPartition / windowReverse                  DiT.swift:113-126
   rope_tables                 RopeTables(headDim: 128)                          DiT.swift:52-97
   qkv_epilogue                normQ/normK + ropeApply + windowPartition          DiT.swift:34-47,100-118,496-506
+  linear                      Linear (+ GELU tanh) on hipBLASLt                  DiT.swift:319-321,371
+  DiTBlock                    DiTBlock + blockForward (streaming)               DiT.swift:363-375,491-551
 Token tensors are (L, H*128) or (1, L, H*128), window order, float32 or bfloat16, on a HIP device, contiguous.
 Every call runs the HIP kernels of libfvsr_lcsa.so; there is no CPU fallback.
 """
@@ -28,7 +30,7 @@ from ._abi import (ATTN_AUTO, ATTN_DENSE, ATTN_KERNEL, DTYPE_BF16, DTYPE_F32, LA
 __all__ = ["FVSRError", "Context", "local_block_mask", "draft_block_mask_and_probs", "draft_block_mask",
            "kernel_block_attention", "block_masked_attention", "block_sparse_attention", "FlashVSRAttentionOps",
            "KVRing", "window_partition", "window_reverse", "attention_mode_auto", "workspace_size",
-           "rope_tables", "rope_tables_device", "qkv_epilogue",
+           "rope_tables", "rope_tables_device", "qkv_epilogue", "linear", "DiTBlock",
            "ATTN_AUTO", "ATTN_DENSE", "ATTN_KERNEL", "LAYOUT_GRID", "LAYOUT_WINDOWS", "lib"]
 
 HEAD_DIM = 128
@@ -399,3 +401,75 @@ class KVRing:
              n_new_slices, layout, q_slices, _ptr(self.ctx.local_device(local)), topk, mode, _ptr(o), _ptr(mask),
              _ptr(probs), _stream(stream))
         return o, mask, probs
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# (f3) the dense parts of the DiT block
+# ---------------------------------------------------------------------------------------------------------------
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, gelu: bool = False,
+           stream=None, out=None) -> torch.Tensor:
+    """`Linear` (y = x W^T + b, W (out, in)) on hipBLASLt in bf16 with fp32 accumulation; gelu applies the tanh-form
+    GELU of the FFN (DiT.swift:371) to the fp32 result. x: (rows, in) bf16 on the device."""
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise FVSRError(_abi.ERR_UNSUPPORTED, "linear", "bf16 operands only")
+    if x.dim() != 2 or not x.is_contiguous() or not weight.is_contiguous():
+        raise FVSRError(_abi.ERR_INVALID_ARG, "linear", "expected contiguous (rows, in) x and (out, in) weight")
+    n_out, n_in = weight.shape
+    if x.shape[1] != n_in:
+        raise FVSRError(_abi.ERR_INVALID_ARG, "linear", f"x has {x.shape[1]} features, weight expects {n_in}")
+    y = torch.empty((x.shape[0], n_out), dtype=x.dtype, device=x.device) if out is None else out
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    ctx = Context.get(x.device)
+    call("fvsr_linear", ctx.handle, _ptr(x), x.shape[0], n_in, _ptr(weight), n_out, _ptr(b), 1 if gelu else 0,
+         _ptr(y), _stream(stream))
+    return y
+
+
+class DiTBlock:
+    """One `DiTBlock` (DiT.swift:363-375) with its weights on the device (bf16), run by `forward` as the streaming
+    `blockForward` (DiT.swift:491-551) over a KVRing layer. `weights` maps the field names of
+    fvsr_dit_block_weights (q_weight, q_bias, ..., ffn2_bias; see DIT_WEIGHT_FIELDS) to tensors; the cross
+    K/V come from `set_context` (CrossAttention.initCache, DiT.swift:346-350)."""
+
+    def __init__(self, weights: dict, heads: int, eps: float = 1e-6):
+        self.heads = heads
+        self.eps = eps
+        self.t = {k: v.to(torch.bfloat16).contiguous() for k, v in weights.items() if v is not None}
+        self.ffn_dim = int(self.t["ffn1_weight"].shape[0])
+        self.ctx_len = 0
+
+    def _struct(self) -> _abi.DiTBlockWeights:
+        w = _abi.DiTBlockWeights()
+        for name, _ in _abi.DiTBlockWeights._fields_:
+            if name in ("ctx_len", "ffn_dim"):
+                continue
+            setattr(w, name, self.t[name].data_ptr() if name in self.t else None)
+        w.ctx_len = self.ctx_len
+        w.ffn_dim = self.ffn_dim
+        return w
+
+    def set_context(self, context: torch.Tensor, stream=None):
+        """context: (ctx_len, C) bf16 text-embedded prompt -> cached cross K/V."""
+        ctxt = _tokens(context.to(torch.bfloat16).contiguous(), "context")
+        n = ctxt.shape[0]
+        self.t["cross_k"] = torch.empty_like(ctxt)
+        self.t["cross_v"] = torch.empty_like(ctxt)
+        self.ctx_len = 0
+        w = self._struct()
+        ctx = Context.get(ctxt.device)
+        call("fvsr_dit_cross_kv", ctx.handle, C.byref(w), self.heads, _ptr(ctxt), n, float(self.eps),
+             _ptr(self.t["cross_k"]), _ptr(self.t["cross_v"]), _stream(stream))
+        self.ctx_len = n
+
+    def forward(self, ring: "KVRing", layer: int, x: torch.Tensor, t_mod: torch.Tensor, n_new_slices: int, t0: int,
+                local, topk: int, mode: int = ATTN_AUTO, theta: float = 10000.0, stream=None) -> torch.Tensor:
+        """x: (L, C) bf16 tokens in natural (f, h, w) order, updated in place and returned; t_mod: (6, C)."""
+        x2 = _tokens(x, "x")
+        if x2.dtype != torch.bfloat16:
+            raise FVSRError(_abi.ERR_UNSUPPORTED, "DiTBlock.forward", "bf16 tokens only")
+        tm = t_mod.to(torch.bfloat16).reshape(6, -1).contiguous()
+        tab = rope_tables_device(x2.device, theta)
+        w = self._struct()
+        call("fvsr_dit_block", ring.ctx.handle, ring.handle, layer, C.byref(w), _ptr(tm), _ptr(x2), n_new_slices, t0,
+             float(self.eps), _ptr(tab), _ptr(ring.ctx.local_device(local)), topk, mode, _stream(stream))
+        return x

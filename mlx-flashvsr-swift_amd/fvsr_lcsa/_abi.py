@@ -49,9 +49,25 @@ SIGNATURES = {
     "fvsr_kv_ring_append_qkv": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _vp]),
     "fvsr_lcsa_layer_qkv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _i, _i, _vp,
                                  _vp, _vp, _vp, _vp]),
+    "fvsr_linear": (_i, [_vp, _vp, _i64, _i, _vp, _i, _vp, _i, _vp, _vp]),
+    "fvsr_dit_cross_kv": (_i, [_vp, _vp, _i, _vp, _i, C.c_float, _vp, _vp, _vp]),
+    "fvsr_dit_block": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, C.c_float, _vp, _vp, _i, _i, _vp]),
     "fvsr_window_partition": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
     "fvsr_window_reverse": (_i, [_i, _vp, _vp, _i, _i, _i, _i, _vp]),
 }
+
+
+# struct fvsr_dit_block_weights, field for field
+DIT_WEIGHT_FIELDS = ["modulation", "q_weight", "q_bias", "k_weight", "k_bias", "v_weight", "v_bias", "o_weight",
+                     "o_bias", "norm_q_weight", "norm_k_weight", "cross_q_weight", "cross_q_bias", "cross_k_weight",
+                     "cross_k_bias", "cross_v_weight", "cross_v_bias", "cross_o_weight", "cross_o_bias",
+                     "cross_norm_q_weight", "cross_norm_k_weight", "cross_k", "cross_v"]
+
+
+class DiTBlockWeights(C.Structure):
+    _fields_ = ([(n, _vp) for n in DIT_WEIGHT_FIELDS] + [("ctx_len", _i)] +
+                [(n, _vp) for n in ["norm3_weight", "norm3_bias", "ffn1_weight", "ffn1_bias", "ffn2_weight",
+                                    "ffn2_bias"]] + [("ffn_dim", _i)])
 
 
 class FVSRError(RuntimeError):
