@@ -48,6 +48,9 @@ def parse_args():
     ap.add_argument("--from-projections", action="store_true",
                     help="with --stream: feed each layer the q/k/v projections in natural token order "
                          "(normQ/normK + RoPE + window partition + ring append fused, output window-reversed)")
+    ap.add_argument("--full-blocks", action="store_true",
+                    help="with --stream: run whole DiT blocks (norms, modulation, projections, LCSA layer call, "
+                         "cross-attention over 512 context tokens, FFN) with random-init weights, 30 of them")
     ap.add_argument("--epilogue", action="store_true",
                     help="time the fused QKV epilogue into the KV ring on one 1920x1152 streaming chunk (HBM-bound)")
     ap.add_argument("--block", action="store_true",
@@ -293,6 +296,87 @@ def epilogue_bench(args):
         "algorithmic_bytes": nbytes}), flush=True)
 
 
+def _random_block(torch, dev, gen, C, F, H, n_ctx, fvsr_lcsa):
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(shape, generator=gen, device=dev) * scale).to(torch.bfloat16)
+
+    W = {"modulation": rnd(6, C, scale=0.1)}
+    for p in ("q", "k", "v", "o", "cross_q", "cross_k", "cross_v", "cross_o"):
+        W[p + "_weight"] = rnd(C, C, scale=C ** -0.5)
+        W[p + "_bias"] = rnd(C, scale=0.05)
+    for p in ("norm_q", "norm_k", "cross_norm_q", "cross_norm_k", "norm3"):
+        W[p + "_weight"] = (1 + 0.1 * torch.randn(C, generator=gen, device=dev)).to(torch.bfloat16)
+    W["norm3_bias"] = rnd(C, scale=0.05)
+    W["ffn1_weight"], W["ffn1_bias"] = rnd(F, C, scale=C ** -0.5), rnd(F, scale=0.05)
+    W["ffn2_weight"], W["ffn2_bias"] = rnd(C, F, scale=F ** -0.5), rnd(C, scale=0.05)
+    blk = fvsr_lcsa.DiTBlock(W, H)
+    blk.set_context(rnd(n_ctx, C))
+    return blk
+
+
+def stream_blocks_bench(args):
+    """The streaming DiT's blocks end to end at 1920x1152 (DiT.swift:556-578 without the patch embedding and head):
+    30 random-init Wan2.1-1.3B-shaped blocks (dim 1536, 12 heads, FFN 8960, 512 context tokens), a first chunk of
+    3 slices then 4 chunks of 1 slice (Pipeline.swift:95-102), each chunk's tokens through every block in turn
+    (blockForward: norms, modulation, projections, LCSA layer call on the block's ring layer, cross-attention, FFN).
+    FLOPs of a steady chunk: 30 x (1.4405 GEMM + 0.0544 cross-attention + 1.6306 LCSA kept) = 93.77 TFLOP."""
+    import torch
+
+    import fvsr_lcsa
+    from fvsr_lcsa import synth
+
+    dev = torch.device("cuda:0")
+    H, bh, bw, F, n_ctx = 12, 9, 15, 8960, 512
+    C, s = H * 128, bh * bw
+    lat_h, lat_w = 8 * bh, 8 * bw
+    local = fvsr_lcsa.local_block_mask(bh, bw, 11)
+    topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    blocks = [_random_block(torch, dev, gen, C, F, H, n_ctx, fvsr_lcsa) for _ in range(args.layers)]
+    t_mod = (torch.randn((6, C), generator=gen, device=dev) * 0.1).to(torch.bfloat16)
+    ring = fvsr_lcsa.KVRing(args.layers, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    chunks = [(3, 0), (1, 6), (1, 8), (1, 10), (1, 12)]
+    xs = [(torch.randn((2 * n * lat_h * lat_w, C), generator=gen, device=dev)).to(torch.bfloat16) for n, _ in chunks]
+
+    def run(events=None):
+        ring.reset()
+        for c, (n, t0) in enumerate(chunks):
+            x = xs[c].clone()
+            if events is not None:
+                events[c][0].record()
+            for layer, blk in enumerate(blocks):
+                blk.forward(ring, layer, x, t_mod, n, t0, local, topk)
+            if events is not None:
+                events[c][1].record()
+            if not torch.isfinite(x.float()).all():
+                raise RuntimeError("DiT blocks produced non-finite tokens")
+
+    run()   # warm-up: workspaces, GEMM algorithms
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 10)
+    tot = [0.0] * len(chunks)
+    for _ in range(reps):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunks]
+        run(ev)
+        torch.cuda.synchronize()
+        for c, (a0, a1) in enumerate(ev):
+            tot[c] += a0.elapsed_time(a1) / reps
+    steady = tot[1:]
+    L = s * 128   # tokens of a steady chunk: one slice = 2 latent frames
+    per_block = 2.0 * L * (6 * C * C + 2 * C * F) + 4.0 * L * n_ctx * C + 4.0 * 128 ** 3 * H * topk
+    print(json.dumps({
+        "metric": "streaming DiT blocks per chunk, 1920x1152 (30 blocks: norms, modulation, projections, LCSA, "
+                  "cross-attention, FFN)",
+        "unit": "ms per chunk (all blocks)", "value": round(sum(steady) / len(steady), 3), "higher_is_better": False,
+        "n_gpus": 1, "dtype": "bf16", "data": "synthetic tokens, random-init weights (no checkpoint)",
+        "config": {"workload": "stream_blocks_1920x1152_bf16", "blocks": args.layers, "heads": H, "dim": C,
+                   "ffn_dim": F, "context_tokens": n_ctx, "topk": topk, "local_range": 11, "kv_window_slices": 3},
+        "chunk_ms": [round(t, 3) for t in tot],
+        "per_block_ms": [round(t / args.layers, 4) for t in tot],
+        "steady_effective_tflops": round(args.layers * per_block / (sum(steady) / len(steady) * 1e-3) / 1e12, 1),
+        "reps": reps}), flush=True)
+
+
 def block_bench(args):
     """One streaming `blockForward` (DiT.swift:491-551) of the Wan2.1-1.3B-shaped DiT (dim 1536, 12 heads, FFN 8960,
     512 context tokens) on a steady 1920x1152 chunk: 2 latent frames = 17280 tokens, KV window of 3 slices + the new
@@ -316,17 +400,7 @@ def block_bench(args):
     def rnd(*shape, scale=1.0):
         return (torch.randn(shape, generator=gen, device=dev) * scale).to(torch.bfloat16)
 
-    W = {"modulation": rnd(6, C, scale=0.1)}
-    for p in ("q", "k", "v", "o", "cross_q", "cross_k", "cross_v", "cross_o"):
-        W[p + "_weight"] = rnd(C, C, scale=C ** -0.5)
-        W[p + "_bias"] = rnd(C, scale=0.05)
-    for p in ("norm_q", "norm_k", "cross_norm_q", "cross_norm_k", "norm3"):
-        W[p + "_weight"] = (1 + 0.1 * torch.randn(C, generator=gen, device=dev)).to(torch.bfloat16)
-    W["norm3_bias"] = rnd(C, scale=0.05)
-    W["ffn1_weight"], W["ffn1_bias"] = rnd(F, C, scale=C ** -0.5), rnd(F, scale=0.05)
-    W["ffn2_weight"], W["ffn2_bias"] = rnd(C, F, scale=F ** -0.5), rnd(C, scale=0.05)
-    blk = fvsr_lcsa.DiTBlock(W, H)
-    blk.set_context(rnd(n_ctx, C))
+    blk = _random_block(torch, dev, gen, C, F, H, n_ctx, fvsr_lcsa)
     t_mod = rnd(6, C, scale=0.1)
     ring = fvsr_lcsa.KVRing(1, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
     x0 = rnd(6 * lat_h * lat_w, C)
@@ -378,6 +452,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.stream and args.full_blocks:
+        stream_blocks_bench(args)
         return
     if args.stream:
         stream_bench(args)
