@@ -7,6 +7,7 @@
 //   flashvsr::LCSA::blockMaskedAttention         blockMaskedAttention(q:k:v:blockMask:...)  DiT.swift:279-313
 //   flashvsr::FlashVSRAttention / current()      FlashVSRAttention (FLASHVSR_ATTN)          DiT.swift:193-203
 //   flashvsr::WindowKVCache                      the per-block window cache of blockForward  DiT.swift:507-511,532-538
+//   flashvsr::DiTBlock                           DiTBlock + the streaming blockForward       DiT.swift:363-375,491-551
 //
 // The reference traps on bad shapes (precondition); here a non-zero fvsr_status throws flashvsr::LCSAError carrying
 // the status and fvsr_last_error(). Device buffers are caller-owned HIP allocations.
@@ -143,11 +144,44 @@ class WindowKVCache {
   }
 
   fvsr_kv_ring* handle() const { return ring_; }
+  LCSA& lcsa() const { return lcsa_; }
 
  private:
   LCSA& lcsa_;
   fvsr_kv_ring* ring_ = nullptr;
   int heads_, s_;
+};
+
+// `DiTBlock` (DiT.swift:363-375) over caller-owned bf16 device tensors: `weights` holds every field of
+// fvsr_dit_block_weights but the cross K/V, which initCache() computes from the text-embedded prompt
+// (CrossAttention.initCache, DiT.swift:346-350) into caller-provided (ctxLen, C) buffers. forward() is the
+// streaming blockForward (DiT.swift:491-551) on tokens x (natural order), updated in place.
+class DiTBlock {
+ public:
+  DiTBlock(const fvsr_dit_block_weights& weights, int heads, float eps = 1e-6f)
+      : w_(weights), heads_(heads), eps_(eps) {}
+
+  void initCache(LCSA& lcsa, const void* context, int ctxLen, void* crossK, void* crossV,
+                 hipStream_t stream = nullptr) {
+    check(fvsr_dit_cross_kv(lcsa.handle(), &w_, heads_, context, ctxLen, eps_, crossK, crossV, stream),
+          "fvsr_dit_cross_kv");
+    w_.cross_k = crossK;
+    w_.cross_v = crossV;
+    w_.ctx_len = ctxLen;
+  }
+
+  void forward(WindowKVCache& cache, int layer, void* x, const void* tMod, int newSlices, int t0,
+               const float* ropeTables, const uint8_t* localDev, int topk,
+               FlashVSRAttention mode = currentAttention(), hipStream_t stream = nullptr) {
+    check(fvsr_dit_block(cache.lcsa().handle(), cache.handle(), layer, &w_, tMod, x, newSlices, t0, eps_, ropeTables,
+                         localDev, topk, static_cast<int>(mode), stream),
+          "fvsr_dit_block");
+  }
+
+ private:
+  fvsr_dit_block_weights w_;
+  int heads_;
+  float eps_;
 };
 
 }  // namespace flashvsr
