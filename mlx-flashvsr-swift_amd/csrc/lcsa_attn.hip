@@ -108,10 +108,13 @@ constexpr int kVRing = kSlots * kTileBytes;            // byte offset of the V r
 constexpr float kMaskedScore = -1.2676506e30f;         // -2^100: exp2 of a masked key is exactly 0
 
 // 16-byte chunk swizzles. K: the 8 (or 16) lanes one ds_read_b128 cycle serves read 8 (16) consecutive rows of one
-// chunk -> distinct positions. V: a ds_read_b64_tr_b16 16-lane group reads 4 consecutive rows (a multiple of 4
-// apart) x 2 adjacent chunks -> 4 distinct chunk pairs.
+// chunk -> distinct positions. V: a ds_read_b64_tr_b16 half-wave (32 lanes, 256 B, one pass over the 64 banks of a
+// 256-byte row) reads 4 consecutive rows (a multiple of 4 apart) x 4 adjacent chunks (two 16-lane groups of 2):
+// XOR-ing the chunk index with 4 * (row mod 4) puts the 4 rows' aligned 4-chunk groups on 4 different groups, so the
+// 32 lanes cover all 64 banks once (the SQ_LDS_BANK_CONFLICT counter reads 0; the former (2 * row) mod 16 swizzle
+// left every second cycle a conflict).
 __device__ __forceinline__ int swz_k(int r) { return r & 15; }
-__device__ __forceinline__ int swz_v(int r) { return (r << 1) & 15; }
+__device__ __forceinline__ int swz_v(int r) { return (r & 3) << 2; }
 
 // s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
 #define FVSR_WAIT_VM_LGKM0(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | (7 << 4))
@@ -263,7 +266,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 #pragma unroll
   for (int t = 0; t < 8; ++t) k_off[t] = l32 * kRowBytes + (((2 * t + g) ^ swz_k(l32)) << 4);
   const int G = lane >> 4, mm = lane & 15;
-  const int vr = 4 * (G >> 1) + (mm >> 2);   // + 16u + 8ab: the swizzle depends on the row mod 8 only
+  const int vr = 4 * (G >> 1) + (mm >> 2);   // + 16u + 8ab: the swizzle depends on the row mod 4 only
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
     v_off[dt] = vr * kRowBytes + (((4 * dt + 2 * (G & 1) + ((mm & 3) >> 1)) ^ swz_v(vr)) << 4) + (mm & 1) * 8;
