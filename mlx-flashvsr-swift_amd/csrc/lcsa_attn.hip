@@ -106,6 +106,7 @@ constexpr int kTileBytes = kTileKeys * kRowBytes;      // 8 KB
 constexpr int kSlots = 4;                              // per ring: slot of tile T = T mod 4 = its quarter of the block
 constexpr int kVRing = kSlots * kTileBytes;            // byte offset of the V ring
 constexpr float kMaskedScore = -1.2676506e30f;         // -2^100: exp2 of a masked key is exactly 0
+constexpr int kMaxPersistentWgs = 1024;                // persistent grid cap (the order kernel's first-row deal)
 
 // 16-byte chunk swizzles. K: the 8 (or 16) lanes one ds_read_b128 cycle serves read 8 (16) consecutive rows of one
 // chunk -> distinct positions. V: a ds_read_b64_tr_b16 half-wave (32 lanes, 256 B, one pass over the 64 banks of a
@@ -163,13 +164,21 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int rows = a.heads * a.nq;
-  // Persistent: the grid is sized to the resident workgroups; each takes the next row (head, query block) from the
-  // list ordered longest key list first, so the long rows start early and the short ones fill in behind them.
+  // Persistent: the grid is sized to the resident workgroups. Workgroup b starts on item b (attn_order_kernel puts
+  // the longest rows there, dealt by XCD), then takes the next item from the counter, longest key list first, so
+  // the long rows start early and the short ones fill in behind them.
+  bool first_item = true;
   for (;;) {
-  if (tid == 0) item_s = atomicAdd(counter, 1);
-  __syncthreads();
-  const int item = item_s;
-  __syncthreads();
+  int item;
+  if (first_item) {
+    item = blockIdx.x;
+    first_item = false;
+  } else {
+    if (tid == 0) item_s = atomicAdd(counter, 1);
+    __syncthreads();
+    item = item_s;
+    __syncthreads();
+  }
   if (item >= rows) break;
   const int row_id = order[item];
   const int h = row_id / a.nq, qb = row_id - h * a.nq;
@@ -569,12 +578,15 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   }   // next row
 }
 
-// Rows (head, query block) ordered by decreasing key-list length for the persistent bf16 walk, and its work counter
-// reset to 0. One workgroup: counting sort over the list length in bins of 8 blocks (the dense walk: every
-// non-empty row is a full walk). Inside a bin rows come out close to row order (head-major, neighbouring query
-// blocks together), so the workgroups running at once share key blocks in L2; the order does not affect results.
+// Rows (head, query block) for the persistent bf16 walk, and its work counter. One workgroup. First a counting sort
+// by decreasing key-list length in bins of 8 blocks (the dense walk: every non-empty row is a full walk). The first
+// `grid` rows of that order are each workgroup's first row (workgroup b takes item b without the counter): they are
+// re-sorted by row id (head-major, neighbouring query blocks together) and dealt so that the workgroups of one XCD
+// (b % 8, dispatch is round-robin over the XCDs) start on one contiguous range of rows, whose key lists overlap, so
+// the XCD's L2 serves the key blocks they share. The counter then hands out the rest, longest first, from item
+// `grid` on. The order does not affect results.
 __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
-                                                          int dense, int32_t* __restrict__ order,
+                                                          int dense, int grid, int32_t* __restrict__ order,
                                                           int32_t* __restrict__ counter) {
   constexpr int kBins = 4096;
   __shared__ int bin_start[kBins];
@@ -611,8 +623,35 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
     run += v[i];
   }
   __syncthreads();
-  for (int r = tid; r < rows; r += 1024) order[atomicAdd(&bin_start[bin_of(r)], 1)] = r;
-  if (tid == 0) *counter = 0;
+  // the first n_first items (one per workgroup) stay in LDS: re-sorted by row id, they are dealt so that XCD x
+  // (workgroups b with b % 8 == x) holds one contiguous range of them
+  const int n_first = min(min(grid, rows), kMaxPersistentWgs);
+  __shared__ __attribute__((aligned(16))) int first[kMaxPersistentWgs];   // padded with INT_MAX (ranks nothing)
+  for (int i = n_first + tid; i < kMaxPersistentWgs; i += 1024) first[i] = 0x7fffffff;
+  for (int r = tid; r < rows; r += 1024) {
+    const int pos = atomicAdd(&bin_start[bin_of(r)], 1);
+    if (pos < n_first) first[pos] = r;
+    else order[pos] = r;
+  }
+  __syncthreads();
+  const int n4 = (n_first + 31) / 32 * 8;   // int4 groups to scan, a multiple of the unroll
+  for (int i = tid; i < n_first; i += 1024) {
+    const int r = first[i];
+    int rank = 0;   // rows are distinct: ranks are a permutation of 0 .. n_first - 1
+#pragma unroll 8
+    for (int j = 0; j < n4; ++j) {
+      const int4 f = reinterpret_cast<const int4*>(first)[j];
+      rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+    }
+    // XCD x holds m_x = (n_first - x + 7) / 8 workgroups, b = x, x + 8, ..; ranks s_x .. s_x + m_x - 1 go to it
+    int x = 0, s0 = 0;
+    while (s0 + (n_first - x + kXcds - 1) / kXcds <= rank) {
+      s0 += (n_first - x + kXcds - 1) / kXcds;
+      ++x;
+    }
+    order[(rank - s0) * kXcds + x] = r;
+  }
+  if (tid == 0) *counter = n_first;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -862,10 +901,11 @@ int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t strea
   dim3 grid(nwg), block(256);
   if (dtype == FVSR_DTYPE_BF16) {
     if (!a.order || !a.counter) return set_error(FVSR_ERR_INVALID_ARG, "attention: no workspace for the row order");
-    hipLaunchKernelGGL(attn_order_kernel, dim3(1), dim3(1024), 0, stream, a.kcnt, nwg, a.nk_stride, dense ? 1 : 0,
-                       a.order, a.counter);
     // two workgroups (64 KB of LDS each) are resident per CU
-    const dim3 pgrid(std::min(nwg, 2 * device_cus()));
+    const int pwgs = std::min(nwg, std::min(2 * device_cus(), kMaxPersistentWgs));
+    hipLaunchKernelGGL(attn_order_kernel, dim3(1), dim3(1024), 0, stream, a.kcnt, nwg, a.nk_stride, dense ? 1 : 0,
+                       pwgs, a.order, a.counter);
+    const dim3 pgrid(pwgs);
     if (attn_query_groups() == 2) {
       if (dense)
         hipLaunchKernelGGL((attn_bf16_kernel<true, 2>), pgrid, dim3(128), 0, stream, a, a.kidx, a.kcnt, a.sel,
