@@ -195,12 +195,12 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 3], kb[3], acc, 0, 0, 0);
       }
       const int jj = 16 * wave + li, j = j0 + jj;
-      if (lg < 2 && jj < nj) {   // rows 4 lg .. 4 lg + 3 < 8
+      if (4 * lg < kScoreRows && jj < nj) {   // rows 4 lg .. 4 lg + 3 that are query rows of the group
         const int ksp = j % s;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int r = 4 * lg + v;
-          ss[r * nk + j] = lm[r * sw + ksp] ? acc[v] / sqrt_d : -INFINITY;
+          if (r < kScoreRows) ss[r * nk + j] = lm[r * sw + ksp] ? acc[v] / sqrt_d : -INFINITY;
         }
       }
     }
