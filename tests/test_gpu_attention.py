@@ -89,6 +89,37 @@ def test_ragged_tails(dev, dtype, lq, lk):
     assert _rel(o, ref) <= (FP32_REL if dtype == torch.float32 else BF16_REL)
 
 
+@pytest.mark.parametrize("heads,lqb,oracle", [(12, 42, True), (12, 43, True), (4, 129, True), (12, 86, False)])
+def test_rows_around_the_persistent_grid(dev, heads, lqb, oracle):
+    """Row counts (heads x query blocks) just below, just above and twice the persistent grid of the bf16 walk
+    (2 workgroups per CU): every workgroup's first row is dealt by XCD, the rest come from the longest-first queue.
+    Row lengths vary from empty to full. The outputs start as NaN, so a row the walk skipped or repeated into the
+    wrong place fails; kernel == dense fallback everywhere, and both against the oracle where it is quick."""
+    lk = 3 * 128 + 50
+    gen = torch.Generator().manual_seed(heads * 1000 + lqb)
+    q = torch.randn((lqb * 128, heads * 128), generator=gen).to(torch.bfloat16)
+    k = torch.randn((lk, heads * 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((lk, heads * 128), generator=gen).to(torch.bfloat16)
+    dens = torch.rand((heads, lqb, 1), generator=gen)   # per-row density: lengths 0 .. 4 blocks
+    m = (torch.rand((heads, lqb, 4), generator=gen) < dens).float()
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), m.to(dev)
+    o = torch.full((lqb * 128, heads * 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    od = torch.full_like(o, float("nan"))
+    print(f"  rows {heads * lqb}, kept blocks {int(m.sum())}", flush=True)
+    fvsr_lcsa.kernel_block_attention(qd, kd, vd, md, heads, out=o)
+    fvsr_lcsa.block_masked_attention(qd, kd, vd, md, heads, out=od)
+    torch.cuda.synchronize()
+    assert not torch.isnan(o).any()
+    assert torch.equal(o, od)
+    empty = (m.sum(-1) == 0)                          # (heads, lqb): rows with no listed block are zeros
+    ov = o.float().cpu().view(lqb, 128, heads, 128)
+    for h, i in empty.nonzero().tolist():
+        assert (ov[i, :, h] == 0).all()
+    if oracle:
+        ref = O.block_masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), m.numpy(), heads)
+        assert _rel(o, ref) <= BF16_REL
+
+
 def test_all_empty_mask_gives_zeros(dev):
     heads = 3
     q = torch.randn((256, heads * 128), device=dev)
