@@ -111,7 +111,7 @@ struct fvsr_kv_ring {
   char* layer_k(int l) const { return (char*)k + (size_t)l * layer_tokens() * C * esize(dtype); }
   char* layer_v(int l) const { return (char*)v + (size_t)l * layer_tokens() * C * esize(dtype); }
   float* layer_pooled(int l) const { return pooled + (size_t)l * capacity * s * C; }
-  KeyMap map(int l) const { return KeyMap{head[l], capacity, s}; }
+  KeyMap map(int l) const { return make_key_map(head[l], capacity, s); }
 };
 
 #define FVSR_REQUIRE(cond, status, msg) \
@@ -282,7 +282,7 @@ int fvsr_lcsa_select(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const
   FVSR_REQUIRE(q_slices > 0 && s > 0, FVSR_ERR_INVALID_ARG, "q_slices and s must be > 0");
   const int64_t nk = ceil_div(lk, kBlock);
   FVSR_REQUIRE(nk <= kMaxSelectKeyBlocks, FVSR_ERR_UNSUPPORTED, "too many key blocks for selection");
-  return select_impl(ctx, dtype, qW, lq, nullptr, false, kW, lk, KeyMap{0, 1, 1 << 30}, (int)nk, heads, q_slices,
+  return select_impl(ctx, dtype, qW, lq, nullptr, false, kW, lk, plain_key_map(), (int)nk, heads, q_slices,
                      s, local_dev, topk, mask_out, probs_out, kidx_out, kcnt_out, nullptr, (hipStream_t)stream);
 }
 
@@ -340,7 +340,7 @@ int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, con
   FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
   const int nk = (int)ceil_div(lk, kBlock);
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
-  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, KeyMap{0, 1, 1 << 30}, o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o);
   if ((rc = attach_order(ctx, a, nk))) return rc;
   return launch_attention(dtype, false, a, (hipStream_t)stream);
 }
@@ -362,7 +362,7 @@ int fvsr_lcsa_attention_mask(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq
   hipStream_t st = (hipStream_t)stream;
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   if ((rc = launch_lists_from_mask(block_mask, (int)(heads * nq), (int)nk, kidx, kcnt, sel, st))) return rc;
-  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, KeyMap{0, 1, 1 << 30}, o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, plain_key_map(), o);
   if ((rc = attach_order(ctx, a, nk))) return rc;
   return launch_attention(dtype, mode == FVSR_ATTN_DENSE, a, st);
 }

@@ -43,17 +43,29 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
 }
 
 // Logical key block j of the key range -> first token row of that block in the K/V buffer.
-// Plain buffers: (slot_head 0, capacity 1, slice_blocks >= Nk) gives row j*128.
+// Plain buffers: plain_key_map() (slot_head 0, capacity 1, slice_blocks 65536 >= Nk) gives row j*128.
 // Ring: block j lives in slot (head + j / s) % capacity at block j % s of that slot.
+// The walks evaluate this once per key block, so the division is a multiply: with inv = floor(2^32 / s) + 1 (33 bits
+// for s = 1), floor(j / s) = (j * inv) >> 32 exactly for 0 <= j < 2^16 and 1 <= s <= 2^16 (inv * s = 2^32 + e with 0 < e <= s, so
+// the error term j * e / (s * 2^32) stays below 1 / s). Both hold: K/V buffers and ring layers are below 2 GiB, so a
+// key range has fewer than 2^16 blocks. The ring holds at most `capacity` slices (j / s < capacity), so the slot
+// wraps at most once.
 struct KeyMap {
   int slot_head;
   int capacity;
   int slice_blocks;
+  uint64_t inv;
   __device__ __forceinline__ int64_t row(int j) const {
-    const int slot = (slot_head + j / slice_blocks) % capacity;
-    return ((int64_t)slot * slice_blocks + (j % slice_blocks)) * kBlock;
+    const int q = (int)(((uint64_t)(unsigned)j * inv) >> 32);
+    int slot = slot_head + q;
+    if (slot >= capacity) slot -= capacity;
+    return ((int64_t)slot * slice_blocks + (j - q * slice_blocks)) * kBlock;
   }
 };
+inline KeyMap make_key_map(int slot_head, int capacity, int slice_blocks) {
+  return KeyMap{slot_head, capacity, slice_blocks, (((uint64_t)1) << 32) / (uint64_t)slice_blocks + 1};
+}
+inline KeyMap plain_key_map() { return make_key_map(0, 1, 1 << 16); }
 
 // One block-pooling source of pool_part_kernel (lcsa_select.hip): the fp32 sums of the runs of 32 tokens of the L
 // tokens of x (nb = ceil(L / 128) blocks) go to partial[(b * kPoolParts + part) * C + c].
