@@ -260,13 +260,19 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   };
   // walked block b: buffer offset of its first row (past the buffer past the end of the walk) and its keys taking
   // part (0 if unselected in the dense walk or outside [0, nk); else up to 128, fewer for a ragged last block)
-  auto walk_soff = [&](int b) -> int { return b < nblocks ? block_soff(DENSE ? b : klist[b]) : (int)range; };
-  auto walk_keys = [&](int b) -> int {
+  // A walked block's entry e: its key block index (sparse walk) or its selection byte (dense walk), -1 past the
+  // end. The loop loads each entry one block before it derives the offset and key count from it, so the load's
+  // wait is covered by the waits of the steps in between.
+  auto walk_entry = [&](int b) -> int { return b < nblocks ? (DENSE ? (int)srow[b] : klist[b]) : -1; };
+  auto entry_soff = [&](int b, int e) -> int { return b < nblocks ? block_soff(DENSE ? b : e) : (int)range; };
+  auto entry_keys = [&](int b, int e) -> int {
     if (b >= nblocks) return 0;
-    const int j = DENSE ? b : klist[b];
-    if ((unsigned)j >= (unsigned)a.nk || (DENSE && srow[b] == 0)) return 0;
+    const int j = DENSE ? b : e;
+    if ((unsigned)j >= (unsigned)a.nk || (DENSE && e == 0)) return 0;
     return (int)min<int64_t>(kBlock, a.lk - (int64_t)j * kBlock);
   };
+  auto walk_soff = [&](int b) -> int { return entry_soff(b, walk_entry(b)); };
+  auto walk_keys = [&](int b) -> int { return entry_keys(b, walk_entry(b)); };
   auto sub_valid = [&](int keys, int sub) -> int { return min(max(keys - sub * kTileKeys, 0), kTileKeys); };
 
   // LDS operand addresses within a slot. K: row l32, chunk 2t+g. V^T (ds_read_b64_tr_b16): 16-lane group G, member
@@ -378,6 +384,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     // per walked block: first-row buffer offset and keys taking part, read two blocks ahead of use
     int o0 = walk_soff(0), o1 = walk_soff(1), o2 = walk_soff(2);
     int n0 = walk_keys(0), n1 = walk_keys(1), n2 = walk_keys(2);
+    int e3 = walk_entry(3);
     if (MODE == 0 && DENSE) {
       // the reference comes from the tile the sparse walk starts with (the first tile of the first listed block),
       // so both walks do the same arithmetic on every selected tile and agree bit for bit
@@ -514,7 +521,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
       __builtin_amdgcn_sched_barrier(0);
     };
     for (int b = 0; b < nblocks; ++b) {
-      const int o3 = walk_soff(b + 3), n3 = walk_keys(b + 3);
+      const int o3 = entry_soff(b + 3, e3), n3 = entry_keys(b + 3, e3);
+      e3 = walk_entry(b + 4);
       // step 4b+s: QK tile 4b+s+1, K tile 4b+s+4 (block b+1), V tile 4b+s+2
       step(C0{}, sub_valid(n0, 1), o1, o0 + 2 * sub_bytes, sA, sB, pB, pA);
       step(C1{}, sub_valid(n0, 2), o1 + sub_bytes, o0 + 3 * sub_bytes, sB, sA, pA, pB);
