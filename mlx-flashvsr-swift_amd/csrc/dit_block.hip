@@ -85,17 +85,26 @@ int linear_bf16(void* state, const void* x, int64_t L, int K, const void* w, int
       fail("hipblasLtMatmulDescCreate failed");
       break;
     }
+    // every attribute must take: a dropped epilogue or bias would compute a different function without an error
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
-    hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
     hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_DEFAULT;
     if (epilogue == 1) ep = bias ? HIPBLASLT_EPILOGUE_GELU_BIAS : HIPBLASLT_EPILOGUE_GELU;
     else if (bias) ep = HIPBLASLT_EPILOGUE_BIAS;
-    hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
-    if (bias) {
-      const hipDataType bt = HIP_R_16BF;
-      hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
-      hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+    const hipDataType bt = HIP_R_16BF;
+    bool ok = hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) ==
+                  HIPBLAS_STATUS_SUCCESS &&
+              hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep)) ==
+                  HIPBLAS_STATUS_SUCCESS;
+    if (ok && bias)
+      ok = hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) ==
+               HIPBLAS_STATUS_SUCCESS &&
+           hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt)) ==
+               HIPBLAS_STATUS_SUCCESS;
+    if (!ok) {
+      fail("hipblasLtMatmulDescSetAttribute failed (transpose, epilogue or bias)");
+      break;
     }
     if (hipblasLtMatrixLayoutCreate(&la, HIP_R_16BF, K, N, K) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatrixLayoutCreate(&lb, HIP_R_16BF, K, L, K) != HIPBLAS_STATUS_SUCCESS ||
@@ -107,12 +116,17 @@ int linear_bf16(void* state, const void* x, int64_t L, int K, const void* w, int
     auto it = b->algos.find(key);
     if (it == b->algos.end()) {
       hipblasLtMatmulPreference_t pref = nullptr;
-      hipblasLtMatmulPreferenceCreate(&pref);
+      if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) {
+        fail("hipblasLtMatmulPreferenceCreate failed");
+        break;
+      }
       uint64_t wsb = b->ws_bytes;
-      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
       hipblasLtMatmulHeuristicResult_t heur[1];
       int n = 0;
-      const hipblasStatus_t hs = hipblasLtMatmulAlgoGetHeuristic(b->handle, desc, la, lb, lc, lc, pref, 1, heur, &n);
+      hipblasStatus_t hs =
+          hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb));
+      if (hs == HIPBLAS_STATUS_SUCCESS)
+        hs = hipblasLtMatmulAlgoGetHeuristic(b->handle, desc, la, lb, lc, lc, pref, 1, heur, &n);
       hipblasLtMatmulPreferenceDestroy(pref);
       if (hs != HIPBLAS_STATUS_SUCCESS || n < 1) {
         rc = set_error(FVSR_ERR_UNSUPPORTED, "hipBLASLt has no algorithm for a " + std::to_string(L) + " x " +
