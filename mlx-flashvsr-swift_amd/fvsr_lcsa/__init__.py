@@ -59,6 +59,19 @@ def _ptr(t) -> C.c_void_p:
     return C.c_void_p(0 if t is None else t.data_ptr())
 
 
+def _on_device(t: torch.Tensor, name: str, device: torch.device, numel: int | None = None) -> torch.Tensor:
+    """A caller-supplied operand the kernels read through a raw pointer: it must live on the tokens' device, be
+    contiguous and, where the library derives its extent from other arguments, hold exactly `numel` elements (the
+    C ABI cannot check a buffer's size, and a short one would be read past its end)."""
+    if not t.is_cuda or t.device != device:
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected a tensor on {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, "expected a contiguous tensor")
+    if numel is not None and t.numel() != numel:
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected {numel} elements, got {t.numel()} (shape {tuple(t.shape)})")
+    return t
+
+
 def _stream(stream) -> C.c_void_p:
     if stream is None:
         stream = torch.cuda.current_stream()
@@ -170,7 +183,8 @@ def _attn_mask(q, k, v, block_mask, heads, mode, stream, out):
     q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
     if not (q2.dtype == k2.dtype == v2.dtype):
         raise FVSRError(_abi.ERR_INVALID_ARG, "attention", "q, k, v dtypes differ")
-    bm = block_mask.to(torch.float32).contiguous()
+    nq, nk = -(-q2.shape[0] // 128), -(-k2.shape[0] // 128)
+    bm = _on_device(block_mask.to(torch.float32).contiguous(), "block_mask", q2.device, heads * nq * nk)
     ctx = Context.get(q2.device)
     o = torch.empty_like(q2) if out is None else _tokens(out, "out")
     call("fvsr_lcsa_attention_mask", ctx.handle, _dtype_code(q2), _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2),
@@ -193,8 +207,12 @@ def block_sparse_attention(q, k, v, kidx, kcnt, heads: int, stream=None, out=Non
     shape = q.shape
     q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
     ctx = Context.get(q2.device)
+    nq = -(-q2.shape[0] // 128)
+    kcnt = _on_device(kcnt.to(torch.int32).contiguous(), "kcnt", q2.device, heads * nq)
     kidx = kidx.to(torch.int32).contiguous()
-    kcnt = kcnt.to(torch.int32).contiguous()
+    if kidx.dim() == 0:
+        raise FVSRError(_abi.ERR_INVALID_ARG, "kidx", "expected (heads, nq, nk_stride) lists")
+    kidx = _on_device(kidx, "kidx", q2.device, heads * nq * kidx.shape[-1])
     o = torch.empty_like(q2) if out is None else _tokens(out, "out")
     call("fvsr_lcsa_attention", ctx.handle, _dtype_code(q2), _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2), k2.shape[0],
          heads, _ptr(kidx), _ptr(kcnt), kidx.shape[-1], _ptr(o), _stream(stream))
@@ -417,8 +435,11 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     n_out, n_in = weight.shape
     if x.shape[1] != n_in:
         raise FVSRError(_abi.ERR_INVALID_ARG, "linear", f"x has {x.shape[1]} features, weight expects {n_in}")
+    _on_device(x, "x", x.device)
+    _on_device(weight, "weight", x.device)
     y = torch.empty((x.shape[0], n_out), dtype=x.dtype, device=x.device) if out is None else out
-    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    _on_device(y, "out", x.device, x.shape[0] * n_out)
+    b = None if bias is None else _on_device(bias.to(torch.bfloat16).contiguous(), "bias", x.device, n_out)
     ctx = Context.get(x.device)
     call("fvsr_linear", ctx.handle, _ptr(x), x.shape[0], n_in, _ptr(weight), n_out, _ptr(b), 1 if gelu else 0,
          _ptr(y), _stream(stream))
@@ -435,8 +456,21 @@ class DiTBlock:
         self.heads = heads
         self.eps = eps
         self.t = {k: v.to(torch.bfloat16).contiguous() for k, v in weights.items() if v is not None}
+        for need in ("q_weight", "ffn1_weight"):
+            if need not in self.t:
+                raise FVSRError(_abi.ERR_INVALID_ARG, "DiTBlock", f"{need} missing")
         self.ffn_dim = int(self.t["ffn1_weight"].shape[0])
         self.ctx_len = 0
+        # every field's extent follows from C and the FFN width: check them here, the kernels only see pointers
+        c, f = int(self.t["q_weight"].shape[0]), self.ffn_dim
+        sizes = {"modulation": 6 * c, "ffn1_weight": f * c, "ffn1_bias": f, "ffn2_weight": c * f}
+        for name in self.t:
+            if name.endswith("_weight") and name not in sizes and "norm" not in name:
+                sizes[name] = c * c
+        dev = self.t["q_weight"].device
+        for name, t in self.t.items():   # cross_k / cross_v are (ctx_len, C), normally from set_context
+            _on_device(t, name, dev, None if name in ("cross_k", "cross_v") else sizes.get(name, c))
+        self.device, self.dim = dev, c
 
     def _struct(self) -> _abi.DiTBlockWeights:
         w = _abi.DiTBlockWeights()
@@ -467,7 +501,8 @@ class DiTBlock:
         x2 = _tokens(x, "x")
         if x2.dtype != torch.bfloat16:
             raise FVSRError(_abi.ERR_UNSUPPORTED, "DiTBlock.forward", "bf16 tokens only")
-        tm = t_mod.to(torch.bfloat16).reshape(6, -1).contiguous()
+        _on_device(x2, "x", self.device, x2.shape[0] * self.dim)
+        tm = _on_device(t_mod.to(torch.bfloat16).reshape(6, -1).contiguous(), "t_mod", self.device, 6 * self.dim)
         tab = rope_tables_device(x2.device, theta)
         w = self._struct()
         call("fvsr_dit_block", ring.ctx.handle, ring.handle, layer, C.byref(w), _ptr(tm), _ptr(x2), n_new_slices, t0,

@@ -120,6 +120,25 @@ def test_rows_around_the_persistent_grid(dev, heads, lqb, oracle):
         assert _rel(o, ref) <= BF16_REL
 
 
+def test_list_and_mask_operands_are_checked(dev):
+    """The C ABI cannot see buffer sizes: the binding rejects lists, masks and outputs whose extent or device does
+    not match the tokens before any pointer reaches a kernel."""
+    heads = 2
+    q = torch.zeros((256, heads * 128), dtype=torch.bfloat16, device=dev)
+    k = torch.zeros((384, heads * 128), dtype=torch.bfloat16, device=dev)
+    kidx = torch.zeros((heads, 2, 3), dtype=torch.int32, device=dev)
+    kcnt = torch.zeros((heads, 2), dtype=torch.int32, device=dev)
+    fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt, heads)          # the right shapes run
+    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx[:, :1], kcnt, heads)   # lists of one query block, two needed
+    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt[:1], heads)
+    with pytest.raises(fvsr_lcsa.FVSRError, match="expected a tensor on"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx.cpu(), kcnt, heads)
+    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+        fvsr_lcsa.kernel_block_attention(q, k, k, torch.ones((heads, 2, 2), device=dev), heads)   # 3 key blocks
+
+
 def test_all_empty_mask_gives_zeros(dev):
     heads = 3
     q = torch.randn((256, heads * 128), device=dev)

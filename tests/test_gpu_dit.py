@@ -59,6 +59,15 @@ def test_linear_rejects_bad_shapes(dev):
         fvsr_lcsa.linear(x, w)          # in_features not a multiple of 8
     with pytest.raises(fvsr_lcsa.FVSRError):
         fvsr_lcsa.linear(x, torch.zeros((16, 8), dtype=torch.bfloat16, device=dev))
+    x16 = torch.zeros((4, 16), dtype=torch.bfloat16, device=dev)
+    w16 = torch.zeros((16, 16), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+        fvsr_lcsa.linear(x16, w16, torch.zeros(8, dtype=torch.bfloat16, device=dev))   # bias shorter than out
+    with pytest.raises(fvsr_lcsa.FVSRError, match="expected a tensor on"):
+        fvsr_lcsa.linear(x16, w16.cpu())                                                # weight on the host
+    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+        fvsr_lcsa.DiTBlock({"q_weight": w16, "ffn1_weight": torch.zeros((32, 16), dtype=torch.bfloat16, device=dev),
+                            "ffn2_weight": torch.zeros((16, 16), dtype=torch.bfloat16, device=dev)}, 1)   # not 16 x 32
 
 
 def _weights(r, c, ffn, heads):
