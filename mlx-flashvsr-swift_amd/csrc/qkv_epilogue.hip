@@ -19,6 +19,8 @@
 // butterfly; every lane then normalises, weights and rotates its own channels and writes them to the token's window
 // position. The pooled keys of a ring append are made afterwards by the same pooling kernels as for plain buffers
 // (pool_part_kernel over the new ring slots, pool_finish_kernel), so they are bit-identical to pooling the written K.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace fvsr {
@@ -36,14 +38,17 @@ __device__ __forceinline__ float round_to(float x) {
   return (float)(T)x;
 }
 
-template <typename T>
+// NV = 16-byte vectors per lane (C * sizeof(T) / 16 / 64, rounded up; at most 6): the token's q, k and v stay in
+// registers, so sizing them to the width keeps the register count, and with it the waves in flight, where this
+// memory-bound pass needs them (3 vectors for 1536 bf16 channels).
+template <typename T, int NV>
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t L, int C, int nbh, int nbw,
     int t0, const T* __restrict__ wq, const T* __restrict__ wk, float eps, const float* __restrict__ rope,
     T* __restrict__ q_out, T* __restrict__ k_out, T* __restrict__ v_out, int dst_slot0, int capacity,
     int slice_blocks) {
   constexpr int VN = 16 / sizeof(T);
-  constexpr int kMaxVec = 6;   // vectors per lane: C <= 64 * 6 * VN (1536 channels in fp32, 3072 in bf16)
+  constexpr int kMaxVec = NV;
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);   // natural token index
@@ -139,14 +144,26 @@ int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, 
   const int es = dtype == FVSR_DTYPE_BF16 ? 2 : 4;
   if (C * es / 16 > 64 * 6) return set_error(FVSR_ERR_UNSUPPORTED, "qkv epilogue: at most 384 16-byte vectors per token");
   const dim3 grid((unsigned)ceil_div(L, 4));
-  if (dtype == FVSR_DTYPE_BF16)
-    hipLaunchKernelGGL(qkv_epilogue_kernel<bf16>, grid, dim3(256), 0, stream, (const bf16*)q, (const bf16*)k,
-                       (const bf16*)v, L, C, nbh, nbw, t0, (const bf16*)wq, (const bf16*)wk, eps, rope, (bf16*)q_out,
-                       (bf16*)k_out, (bf16*)v_out, dst_slot0, capacity, slice_blocks);
-  else
-    hipLaunchKernelGGL(qkv_epilogue_kernel<float>, grid, dim3(256), 0, stream, (const float*)q, (const float*)k,
-                       (const float*)v, L, C, nbh, nbw, t0, (const float*)wq, (const float*)wk, eps, rope,
-                       (float*)q_out, (float*)k_out, (float*)v_out, dst_slot0, capacity, slice_blocks);
+  const int nv = (int)ceil_div((int64_t)C * es / 16, 64);   // 1 .. 6, checked above
+  auto go = [&](auto nv_c) {
+    constexpr int NV = decltype(nv_c)::value;
+    if (dtype == FVSR_DTYPE_BF16)
+      hipLaunchKernelGGL((qkv_epilogue_kernel<bf16, NV>), grid, dim3(256), 0, stream, (const bf16*)q,
+                         (const bf16*)k, (const bf16*)v, L, C, nbh, nbw, t0, (const bf16*)wq, (const bf16*)wk, eps,
+                         rope, (bf16*)q_out, (bf16*)k_out, (bf16*)v_out, dst_slot0, capacity, slice_blocks);
+    else
+      hipLaunchKernelGGL((qkv_epilogue_kernel<float, NV>), grid, dim3(256), 0, stream, (const float*)q,
+                         (const float*)k, (const float*)v, L, C, nbh, nbw, t0, (const float*)wq, (const float*)wk,
+                         eps, rope, (float*)q_out, (float*)k_out, (float*)v_out, dst_slot0, capacity, slice_blocks);
+  };
+  switch (nv) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    case 4: go(std::integral_constant<int, 4>{}); break;
+    case 5: go(std::integral_constant<int, 5>{}); break;
+    default: go(std::integral_constant<int, 6>{}); break;
+  }
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }

@@ -286,8 +286,8 @@ def qkv_epilogue(q, k, v, f: int, h: int, w: int, heads: int, t0: int, norm_q_we
     (DiT.swift:34-47,100-118,496-506). Returns (q_out, k_out, v_out)."""
     q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
     ctx = Context.get(q2.device)
-    wq = norm_q_weight.to(q2.dtype).contiguous()
-    wk = norm_k_weight.to(q2.dtype).contiguous()
+    wq = _on_device(norm_q_weight.to(q2.dtype).contiguous(), "norm_q_weight", q2.device, q2.shape[1])
+    wk = _on_device(norm_k_weight.to(q2.dtype).contiguous(), "norm_k_weight", q2.device, q2.shape[1])
     tab = rope_tables_device(q2.device, theta)
     qo, ko, vo = torch.empty_like(q2), torch.empty_like(k2), torch.empty_like(v2)
     call("fvsr_qkv_epilogue", ctx.handle, _dtype_code(q2), _ptr(q2), _ptr(k2), _ptr(v2), f, h, w, heads, t0,
