@@ -642,14 +642,50 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
     else order[pos] = r;
   }
   __syncthreads();
+  // rank of each first row among them by row id: a bitmap over the row ids (the bin counts are free now) and a scan
+  // of its per-word popcounts; beyond 32 x 4096 rows, a scan of the first rows themselves
+  const bool use_bitmap = rows <= kBins * 32;
+  __shared__ int wpre[kBins];   // set bits in the words before word w
+  unsigned* const bm = (unsigned*)bin_start;
+  if (use_bitmap) {
+    for (int w = tid; w < kBins; w += 1024) bm[w] = 0u;
+    __syncthreads();
+    for (int i = tid; i < n_first; i += 1024) atomicOr(&bm[first[i] >> 5], 1u << (first[i] & 31));
+    __syncthreads();
+    int c[4], csum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      c[i] = __popc(bm[4 * tid + i]);
+      csum += c[i];
+    }
+    part[tid] = csum;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {
+      const int x = tid >= d ? part[tid - d] : 0;
+      __syncthreads();
+      part[tid] += x;
+      __syncthreads();
+    }
+    int crun = part[tid] - csum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wpre[4 * tid + i] = crun;
+      crun += c[i];
+    }
+    __syncthreads();
+  }
   const int n4 = (n_first + 31) / 32 * 8;   // int4 groups to scan, a multiple of the unroll
   for (int i = tid; i < n_first; i += 1024) {
     const int r = first[i];
     int rank = 0;   // rows are distinct: ranks are a permutation of 0 .. n_first - 1
+    if (use_bitmap) {
+      rank = wpre[r >> 5] + __popc(bm[r >> 5] & ((1u << (r & 31)) - 1u));
+    } else {
 #pragma unroll 8
-    for (int j = 0; j < n4; ++j) {
-      const int4 f = reinterpret_cast<const int4*>(first)[j];
-      rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+      for (int j = 0; j < n4; ++j) {
+        const int4 f = reinterpret_cast<const int4*>(first)[j];
+        rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+      }
     }
     // XCD x holds m_x = (n_first - x + 7) / 8 workgroups, b = x, x + 8, ..; ranks s_x .. s_x + m_x - 1 go to it
     int x = 0, s0 = 0;
