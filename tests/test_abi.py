@@ -113,3 +113,17 @@ def test_rope_tables_rejects_short_buffer():
     out = np.empty(10, dtype=np.float32)
     rc = _abi.lib.fvsr_rope_tables(10000.0, out.ctypes.data_as(C.c_void_p), 10)
     assert rc == _abi.ERR_INVALID_ARG
+
+
+def test_binding_rejects_host_operands_before_any_device_call():
+    """The binding checks where each operand lives before a pointer reaches the library: host tensors are refused
+    (no context is created, so this runs without a GPU)."""
+    import torch
+    x = torch.zeros((4, 16), dtype=torch.bfloat16)
+    w = torch.zeros((16, 16), dtype=torch.bfloat16)
+    with pytest.raises(fvsr_lcsa.FVSRError, match="expected a tensor on") as ei:
+        fvsr_lcsa.linear(x, w)
+    assert ei.value.status == _abi.ERR_INVALID_ARG
+    with pytest.raises(fvsr_lcsa.FVSRError, match="device tensor"):
+        fvsr_lcsa.block_sparse_attention(x, x, x, torch.zeros((1, 1, 1), dtype=torch.int32),
+                                         torch.zeros((1, 1), dtype=torch.int32), 1)
