@@ -2,14 +2,14 @@
 
 A step is one LCSA layer call of the DiT self-attention block on the 1920x1152 workload (bf16, 12 heads x 128,
 Lq 17280 = 2 latent frames, Lk 43200 = 5 latent frames incl. cache, local range 11, 30% of the in-window block pairs
-kept, per-head RMS-normed Q/K with 3-D RoPE): block selection (pool Q and K, block scores, softmax, exact per-(head,
-slice) top-k, key lists) followed by the block-sparse attention over the kept 128x128 blocks. Inputs are resident in
-HBM before the timed region. Throughput counts kept-block FLOPs only (4 * 128 * valid q tokens * valid k tokens per
-kept (head, q-block, k-block)).
+kept; Q/K a smooth low-frequency field plus noise, per-head RMS-normed, with 3-D RoPE): block selection (pool Q and K,
+block scores, softmax, exact per-(head, slice) top-k, key lists) followed by the block-sparse attention over the kept
+128x128 blocks. Inputs are resident in HBM before the timed region. Throughput counts kept-block FLOPs only
+(4 * 128 * valid q tokens * valid k tokens per kept (head, q-block, k-block)).
 
 Printed: one JSON line (rank 0) with the layer-call rate, the attention kernel's MFMA roofline fraction (kernel time
-from HIP events on the launch stream), the same kernel's dense fallback time, and the CPU oracle timed on a bounded
-sample on the host.
+from HIP events on the launch stream), the same kernel's dense fallback (every key block of every row listed), the
+top-k threshold margin of the workload, and the CPU oracle timed on a bounded sample on the host.
 """
 from __future__ import annotations
 
@@ -36,7 +36,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="sparse_1920x1152_bf16")
-    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=None, help="generator seed (default: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="time only the attention kernel loop (profiling)")
@@ -76,9 +76,28 @@ def read_traffic():
     return None
 
 
+def threshold_margin(probs, q_slices: int, topk: int) -> float:
+    """Smallest relative gap, over the (head, query slice) rows, between the top-k threshold (the (k+1)-th largest
+    probability) and the k-th largest, from the selection's own probabilities: the mask is reproducible by any fp32
+    implementation of the same formula when this is far above fp32 rounding."""
+    import torch
+
+    h, nq, nk = probs.shape
+    flat = probs.reshape(h * q_slices, -1)
+    kk = min(flat.shape[1] - 1, topk)
+    top = torch.topk(flat, kk + 1, dim=1).values            # descending
+    thr = top[:, kk]
+    if kk == 0:
+        return float("inf")
+    above = top[:, kk - 1]
+    return float(((above - thr) / above.clamp_min(1e-38)).min().item())
+
+
 def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
     """The oracle on the host: selection over the whole workload plus attention over a sample of (head, query
-    block) rows, scaled to one layer call."""
+    block) rows, scaled to one layer call. The oracle's attention is a per-row masked softmax over the selected key
+    blocks only (a sparse CPU path; the reference's own CPU path, MLX-CPU blockMaskedAttention, computes every
+    block pair and would be slower). Also reports whether the oracle's block mask equals the GPU's bit for bit."""
     import numpy as np
     from threadpoolctl import threadpool_info
 
@@ -89,9 +108,10 @@ def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
     local = synth.local_mask(wl).numpy()
     topk = synth.workload_topk(wl)
     t0 = time.perf_counter()
-    O.draft_block_mask_and_probs(qn, kn, wl.heads, wl.q_slices, wl.s, local, topk, lk=wl.lk)
+    ref_mask, _ = O.draft_block_mask_and_probs(qn, kn, wl.heads, wl.q_slices, wl.s, local, topk, lk=wl.lk)
     t_sel = time.perf_counter() - t0
     m = mask.cpu().numpy()
+    mask_equal = bool(np.array_equal(m, ref_mask))
     rows = [(h, i) for h in range(wl.heads) for i in range(wl.nq)]
     rng = np.random.default_rng(0)
     order = rng.permutation(len(rows))
@@ -117,9 +137,13 @@ def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
         "unit": "TFLOP/s (effective, kept blocks)",
         "ms_per_layer_call": t_layer * 1e3,
         "cores": int(threads),
+        "host_cpus": os.cpu_count(),
+        "host_cpus_usable": len(os.sched_getaffinity(0)),
         "kind": "port",
-        "sample": f"oracle (numpy fp32) selection over the full workload ({t_sel:.2f} s) + block-masked attention "
-                  f"over {len(done)} of {len(rows)} (head, query block) rows ({t_att:.2f} s), scaled by kept FLOPs",
+        "sample": f"oracle (numpy fp32, {threads} BLAS threads) selection over the full workload ({t_sel:.2f} s) + "
+                  f"per-row masked attention over the selected key blocks of {len(done)} of {len(rows)} (head, "
+                  f"query block) rows ({t_att:.2f} s), scaled by kept FLOPs",
+        "mask_equals_gpu": mask_equal,
     }
 
 
@@ -164,7 +188,7 @@ def stream_bench(args):
     local = fvsr_lcsa.local_block_mask(bh, bw, 11)
     topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
     chunks = [(3, 0), (1, 6), (1, 8), (1, 10), (1, 12)]   # (slices, first latent frame)
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    gen = torch.Generator(device=dev).manual_seed(args.seed or 0)
     data = []
     proj = args.from_projections
     wq = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
@@ -260,7 +284,7 @@ def epilogue_bench(args):
     s, C = bh * bw, H * 128
     f, h, w = 2, 8 * bh, 8 * bw
     L = f * h * w
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    gen = torch.Generator(device=dev).manual_seed(args.seed or 0)
     q, k, v = (torch.randn((L, C), generator=gen, device=dev).to(torch.bfloat16) for _ in range(3))
     wq = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
     wk = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
@@ -331,7 +355,7 @@ def stream_blocks_bench(args):
     lat_h, lat_w = 8 * bh, 8 * bw
     local = fvsr_lcsa.local_block_mask(bh, bw, 11)
     topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    gen = torch.Generator(device=dev).manual_seed(args.seed or 0)
     blocks = [_random_block(torch, dev, gen, C, F, H, n_ctx, fvsr_lcsa) for _ in range(args.layers)]
     t_mod = (torch.randn((6, C), generator=gen, device=dev) * 0.1).to(torch.bfloat16)
     ring = fvsr_lcsa.KVRing(args.layers, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
@@ -395,7 +419,7 @@ def block_bench(args):
     lat_h, lat_w = 8 * bh, 8 * bw
     local = fvsr_lcsa.local_block_mask(bh, bw, 11)
     topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
-    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    gen = torch.Generator(device=dev).manual_seed(args.seed or 0)
 
     def rnd(*shape, scale=1.0):
         return (torch.randn(shape, generator=gen, device=dev) * scale).to(torch.bfloat16)
@@ -467,7 +491,8 @@ def main():
         return
     dev = torch.device("cuda:0")
     wl = synth.WORKLOADS[args.workload]
-    q, k, v = synth.make_qkv(wl, seed=args.seed, device=dev)
+    seed = wl.seed if args.seed is None else args.seed
+    q, k, v = synth.make_qkv(wl, seed=seed, device=dev)
     local = synth.local_mask(wl).numpy()
     topk = synth.workload_topk(wl)
     ctx = fvsr_lcsa.Context.get(dev)
@@ -479,15 +504,17 @@ def main():
         return fvsr_lcsa.draft_block_mask_and_probs(q, k, wl.heads, wl.q_slices, wl.s, local, topk,
                                                     want_mask=False, want_probs=False)
 
-    def attend(kidx, kcnt):
-        fvsr_lcsa.block_sparse_attention(q, k, v, kidx, kcnt, wl.heads, out=o)
+    def attend(kidx, kcnt, out=o):
+        fvsr_lcsa.block_sparse_attention(q, k, v, kidx, kcnt, wl.heads, out=out)
 
-    # reference selection for FLOP counting and the dense fallback
-    mask, _, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q, k, wl.heads, wl.q_slices, wl.s, local, topk,
-                                                               want_probs=False)
+    # one selection up front (untimed) for FLOP counting, the threshold margin and the dense fallbacks
+    mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q, k, wl.heads, wl.q_slices, wl.s, local, topk)
     torch.cuda.synchronize()
     kept = synth.kept_flops(kcnt, kidx, wl.lq, wl.lk)
     kept_fraction = float(kcnt.sum().item()) / (wl.heads * wl.nq * wl.nk)
+    margin = threshold_margin(probs, wl.q_slices, topk)
+    empty_rows = int((kcnt == 0).sum().item())
+    del probs
 
     for _ in range(args.warmup):
         _, _, ki, kc = select()
@@ -519,19 +546,30 @@ def main():
     ms_attn = sum(a.elapsed_time(b) for a, b in ev) / args.steps
     ms_select = ms_step - ms_attn
 
-    # dense fallback: the same kernel walking every key block (masked), same inputs
-    od = torch.empty_like(q)
-    for _ in range(2):
-        fvsr_lcsa.block_masked_attention(q, k, v, mask, wl.heads, out=od)
-    torch.cuda.synchronize()
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        d0.record(stream)
+        for _ in range(n):
+            fn()
+        d1.record(stream)
+        torch.cuda.synchronize()
+        return d0.elapsed_time(d1) / n
+
     nd = max(3, args.steps // 4)
-    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    d0.record(stream)
-    for _ in range(nd):
-        fvsr_lcsa.block_masked_attention(q, k, v, mask, wl.heads, out=od)
-    d1.record(stream)
-    torch.cuda.synchronize()
-    ms_dense = d0.elapsed_time(d1) / nd    # includes the mask -> list build (a few us)
+    od = torch.empty_like(q)
+    # dense fallback as the reference's blockMaskedAttention costs it (DiT.swift:279-313): every key block of every
+    # query block listed (kcnt = Nk), the same kernel walking all H x Nq x Nk block pairs
+    kidx_all = torch.arange(wl.nk, dtype=torch.int32, device=dev).repeat(wl.heads, wl.nq, 1).contiguous()
+    kcnt_all = torch.full((wl.heads, wl.nq), wl.nk, dtype=torch.int32, device=dev)
+    ms_dense = timed(lambda: attend(kidx_all, kcnt_all, od), nd)
+    del kidx_all, kcnt_all
+    # the masked dense walk (FVSR_ATTN_DENSE: every key block of each non-empty row, unselected ones masked; rows
+    # that select nothing are written as zeros without a walk); includes the mask -> list build (a few us)
+    ms_masked = timed(lambda: fvsr_lcsa.block_masked_attention(q, k, v, mask, wl.heads, out=od), nd)
+    dense_flops = 4.0 * 128 * wl.heads * wl.lq * wl.lk
 
     achieved = kept / (ms_attn * 1e-3) / 1e12
     value = kept / (ms_step * 1e-3) / 1e12
@@ -548,22 +586,30 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1), per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)",
+        "data": (f"synthetic, seed {seed} ({'smooth field + noise, ' if wl.smooth else 'i.i.d. N(0,1), '}"
+                 "per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)"),
         "config": {
             "workload": wl.name,
             "description": wl.description,
             "heads": wl.heads, "head_dim": 128, "lq": wl.lq, "lk": wl.lk, "q_blocks": wl.nq, "k_blocks": wl.nk,
             "spatial_blocks_per_slice": wl.s, "local_range": wl.local_range, "topk": topk,
             "kept_block_fraction": round(kept_fraction, 4), "kept_tflop": round(kept / 1e12, 4),
+            "empty_rows": empty_rows, "rows": wl.heads * wl.nq,
+            "threshold_margin": float(f"{margin:.4g}"),
         },
         "breakdown_ms": {
             "layer_call": round(ms_step, 4),
             "attention_kernel": round(ms_attn, 4),
             "selection": round(ms_select, 4),
-            "dense_fallback_attention": round(ms_dense, 4),
+            "dense_fallback_all_blocks": round(ms_dense, 4),
+            "dense_masked_walk": round(ms_masked, 4),
         },
         "attention_tflops": round(achieved, 2),
+        "layer_call_frac": round(value / PEAK_BF16_TFLOPS, 4),
         "sparse_vs_dense_speedup": round(ms_dense / ms_attn, 3),
+        "layer_call_vs_dense_speedup": round(ms_dense / ms_step, 3),
+        "sparse_vs_masked_walk_speedup": round(ms_masked / ms_attn, 3),
+        "dense_fallback_tflops": round(dense_flops / (ms_dense * 1e-3) / 1e12, 1),
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),
@@ -571,6 +617,9 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": (f"{os.path.relpath(PROFILE_PMC, ROOT)}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
+                               "the sparse attention kernel, copy-calibrated (not measured in this run)"
+                               if traffic is not None else None),
         },
         "host_wall_s": round(wall, 3),
     }

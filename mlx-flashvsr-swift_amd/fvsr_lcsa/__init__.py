@@ -46,13 +46,29 @@ def _dtype_code(t: torch.Tensor) -> int:
 
 
 def _tokens(x: torch.Tensor, name: str) -> torch.Tensor:
+    """(L, C) view of a token operand (2-D, or 3-D with batch 1), contiguous. Metadata only: where the operands live
+    is checked by _devices right before the library call, after every shape check."""
+    if x is None:
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, "is None")
     if x.dim() == 3:
         if x.shape[0] != 1:
             raise FVSRError(_abi.ERR_UNSUPPORTED, name, "batch 1 only (the reference asserts the same)")
         x = x[0]
-    if x.dim() != 2 or not x.is_cuda or not x.is_contiguous():
-        raise FVSRError(_abi.ERR_INVALID_ARG, name, "expected a contiguous (L, C) device tensor")
+    if x.dim() != 2 or not x.is_contiguous():
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected contiguous (L, C) tokens, got {tuple(x.shape)}")
     return x
+
+
+def _devices(*named) -> torch.device:
+    """Every (tensor, name) operand on the HIP device of the first one, contiguous; None entries are skipped. Runs
+    before any pointer reaches the library: a host tensor's address handed to a kernel would fault the GPU."""
+    first, fname = named[0]
+    if not first.is_cuda:
+        raise FVSRError(_abi.ERR_INVALID_ARG, fname, f"expected a tensor on a HIP device, got {first.device}")
+    for t, n in named:
+        if t is not None:
+            _on_device(t, n, first.device)
+    return first.device
 
 
 def _ptr(t) -> C.c_void_p:
@@ -70,6 +86,24 @@ def _on_device(t: torch.Tensor, name: str, device: torch.device, numel: int | No
     if numel is not None and t.numel() != numel:
         raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected {numel} elements, got {t.numel()} (shape {tuple(t.shape)})")
     return t
+
+
+def _shaped(t: torch.Tensor, name: str, shape: tuple, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Metadata checks of an operand whose extent the library derives from other arguments: exact shape, then
+    dtype. They run before any device check, so a wrong operand is named even for host tensors."""
+    if t is None:
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, "is None")
+    if tuple(t.shape) != tuple(shape):
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected shape {tuple(shape)}, got {tuple(t.shape)}")
+    if dtype is not None and t.dtype != dtype:
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected dtype {dtype}, got {t.dtype}")
+    return t
+
+
+def _heads_width(x: torch.Tensor, name: str, heads: int) -> None:
+    if x.dim() != 2 or x.shape[1] != heads * HEAD_DIM:
+        raise FVSRError(_abi.ERR_INVALID_ARG, name,
+                        f"expected (L, {heads * HEAD_DIM}) tokens for {heads} heads of {HEAD_DIM}, got {tuple(x.shape)}")
 
 
 def _stream(stream) -> C.c_void_p:
@@ -105,12 +139,16 @@ class Context:
     def workspace_bytes(self) -> int:
         return int(lib.fvsr_ctx_workspace_bytes(self.handle))
 
-    def local_device(self, local) -> torch.Tensor:
+    def local_device(self, local, s: int) -> torch.Tensor:
         """Device copy of an (s, s) local window mask, memoised by content (the reference memoises per geometry,
-        DiT.swift:464-470)."""
+        DiT.swift:464-470). The library reads s * s bytes from it."""
         if isinstance(local, torch.Tensor) and local.is_cuda:
-            return local.to(torch.uint8).contiguous()
+            if local.numel() != s * s:
+                raise FVSRError(_abi.ERR_INVALID_ARG, "local", f"expected an ({s}, {s}) mask, got {tuple(local.shape)}")
+            return _on_device(local.to(torch.uint8).contiguous(), "local", torch.device(f"cuda:{self.device}"))
         arr = np.ascontiguousarray(np.asarray(local, dtype=np.uint8))
+        if arr.size != s * s:
+            raise FVSRError(_abi.ERR_INVALID_ARG, "local", f"expected an ({s}, {s}) mask, got {arr.shape}")
         key = (arr.shape, arr.tobytes())
         t = self._local_cache.get(key)
         if t is None:
@@ -157,6 +195,11 @@ def draft_block_mask_and_probs(qW: torch.Tensor, kW: torch.Tensor, heads: int, q
     kcnt (H, Nq) i32). DiT.swift:158-174 + SparseAttention.swift:175-177."""
     q = _tokens(qW.reshape(-1, qW.shape[-1]) if qW.dim() == 3 and qW.shape[0] != 1 else qW, "qW")
     k = _tokens(kW.reshape(-1, kW.shape[-1]) if kW.dim() == 3 and kW.shape[0] != 1 else kW, "kW")
+    _heads_width(q, "qW", heads)
+    _heads_width(k, "kW", heads)
+    if q.dtype != k.dtype:
+        raise FVSRError(_abi.ERR_INVALID_ARG, "kW", f"dtype {k.dtype} differs from qW's {q.dtype}")
+    _devices((q, "qW"), (k, "kW"))
     ctx = Context.get(q.device)
     nq = -(-q.shape[0] // BLOCK)
     nk = -(-k.shape[0] // BLOCK)
@@ -165,7 +208,7 @@ def draft_block_mask_and_probs(qW: torch.Tensor, kW: torch.Tensor, heads: int, q
     probs = torch.empty((heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
     kidx = torch.empty((heads, nq, nk), dtype=torch.int32, device=dev)
     kcnt = torch.empty((heads, nq), dtype=torch.int32, device=dev)
-    loc = ctx.local_device(local)
+    loc = ctx.local_device(local, s)
     call("fvsr_lcsa_select", ctx.handle, _dtype_code(q), _ptr(q), q.shape[0], _ptr(k), k.shape[0], heads, q_slices,
          s, _ptr(loc), topk, _ptr(mask), _ptr(probs), _ptr(kidx), _ptr(kcnt), _stream(stream))
     return mask, probs, kidx, kcnt
@@ -180,16 +223,52 @@ def draft_block_mask(qW, kW, heads, q_slices, s, local, topk, stream=None) -> to
 # ------------------------------------------------------------------------------------------------------------------
 def _attn_mask(q, k, v, block_mask, heads, mode, stream, out):
     shape = q.shape
-    q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
-    if not (q2.dtype == k2.dtype == v2.dtype):
-        raise FVSRError(_abi.ERR_INVALID_ARG, "attention", "q, k, v dtypes differ")
+    q2, k2, v2 = _qkv_operands(q, k, v, heads)
     nq, nk = -(-q2.shape[0] // 128), -(-k2.shape[0] // 128)
-    bm = _on_device(block_mask.to(torch.float32).contiguous(), "block_mask", q2.device, heads * nq * nk)
+    if block_mask.numel() != heads * nq * nk:
+        raise FVSRError(_abi.ERR_INVALID_ARG, "block_mask",
+                        f"expected {heads * nq * nk} elements ({heads}, {nq}, {nk}), got {tuple(block_mask.shape)}")
+    o = _out_meta(out, q2)
+    _devices((q2, "q"), (k2, "k"), (v2, "v"), (block_mask, "block_mask"), (o, "out"))
+    bm = block_mask.to(torch.float32).contiguous()
+    o = torch.empty_like(q2) if o is None else o
     ctx = Context.get(q2.device)
-    o = torch.empty_like(q2) if out is None else _tokens(out, "out")
     call("fvsr_lcsa_attention_mask", ctx.handle, _dtype_code(q2), _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2),
          k2.shape[0], heads, _ptr(bm), mode, _ptr(o), _stream(stream))
     return o.reshape(shape)
+
+
+def _qkv_operands(q, k, v, heads):
+    """(q, k, v) token operands of an attention call: 2-D, heads * 128 wide, one dtype, K and V of one shape."""
+    q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+    for t, n in ((q2, "q"), (k2, "k"), (v2, "v")):
+        _heads_width(t, n, heads)
+    if not (q2.dtype == k2.dtype == v2.dtype):
+        raise FVSRError(_abi.ERR_INVALID_ARG, "attention", "q, k, v dtypes differ")
+    if k2.shape != v2.shape:
+        raise FVSRError(_abi.ERR_INVALID_ARG, "v", f"expected the shape of k {tuple(k2.shape)}, got {tuple(v2.shape)}")
+    return q2, k2, v2
+
+
+def _out_meta(out, ref: torch.Tensor, name: str = "out"):
+    """A caller-supplied output (or None): the shape and dtype of `ref` (a batch-1 3-D view allowed), contiguous."""
+    if out is None:
+        return None
+    o = out[0] if out.dim() == 3 and out.shape[0] == 1 else out
+    _shaped(o, name, tuple(ref.shape), ref.dtype)
+    if not o.is_contiguous():
+        raise FVSRError(_abi.ERR_INVALID_ARG, name, "expected a contiguous tensor")
+    return o
+
+
+def _lists_meta(kidx, kcnt, heads: int, nq: int):
+    """kidx (heads, nq, stride >= 1) and kcnt (heads, nq) of an integer type (int32 is what the library reads)."""
+    if kidx.dim() != 3 or tuple(kidx.shape[:2]) != (heads, nq) or kidx.shape[2] < 1:
+        raise FVSRError(_abi.ERR_INVALID_ARG, "kidx", f"expected ({heads}, {nq}, stride) lists, got {tuple(kidx.shape)}")
+    _shaped(kcnt, "kcnt", (heads, nq))
+    for t, n in ((kidx, "kidx"), (kcnt, "kcnt")):
+        if t.dtype.is_floating_point or t.dtype.is_complex or t.dtype == torch.bool:
+            raise FVSRError(_abi.ERR_INVALID_ARG, n, f"expected an integer tensor, got {t.dtype}")
 
 
 def kernel_block_attention(q, k, v, block_mask, heads: int, stream=None, out=None) -> torch.Tensor:
@@ -205,15 +284,14 @@ def block_masked_attention(q, k, v, block_mask, heads: int, stream=None, out=Non
 def block_sparse_attention(q, k, v, kidx, kcnt, heads: int, stream=None, out=None) -> torch.Tensor:
     """Attention from (kidx, kcnt) lists: the Metal launch ABI of SparseAttention.swift:180-185."""
     shape = q.shape
-    q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
-    ctx = Context.get(q2.device)
+    q2, k2, v2 = _qkv_operands(q, k, v, heads)
     nq = -(-q2.shape[0] // 128)
-    kcnt = _on_device(kcnt.to(torch.int32).contiguous(), "kcnt", q2.device, heads * nq)
-    kidx = kidx.to(torch.int32).contiguous()
-    if kidx.dim() == 0:
-        raise FVSRError(_abi.ERR_INVALID_ARG, "kidx", "expected (heads, nq, nk_stride) lists")
-    kidx = _on_device(kidx, "kidx", q2.device, heads * nq * kidx.shape[-1])
-    o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+    _lists_meta(kidx, kcnt, heads, nq)
+    o = _out_meta(out, q2)
+    _devices((q2, "q"), (k2, "k"), (v2, "v"), (kidx, "kidx"), (kcnt, "kcnt"), (o, "out"))
+    kidx, kcnt = kidx.to(torch.int32).contiguous(), kcnt.to(torch.int32).contiguous()
+    o = torch.empty_like(q2) if o is None else o
+    ctx = Context.get(q2.device)
     call("fvsr_lcsa_attention", ctx.handle, _dtype_code(q2), _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2), k2.shape[0],
          heads, _ptr(kidx), _ptr(kcnt), kidx.shape[-1], _ptr(o), _stream(stream))
     return o.reshape(shape)
@@ -237,6 +315,7 @@ class FlashVSRAttentionOps:
 def _layout(x, f, h, w, to_windows, stream):
     shape = x.shape
     x2 = _tokens(x, "x")
+    _devices((x2, "x"))
     out = torch.empty_like(x2)
     name = "fvsr_window_partition" if to_windows else "fvsr_window_reverse"
     call(name, _dtype_code(x2), _ptr(x2), _ptr(out), f, h, w, x2.shape[1], _stream(stream))
@@ -279,15 +358,29 @@ def rope_tables_device(device, theta: float = 10000.0) -> torch.Tensor:
     return t
 
 
+def _norm_weights(wq, wk, c: int, dtype):
+    """The two WanRMSNorm weights: C elements each, in the tokens' dtype."""
+    out = []
+    for t, n in ((wq, "norm_q_weight"), (wk, "norm_k_weight")):
+        if t is None or t.numel() != c:
+            raise FVSRError(_abi.ERR_INVALID_ARG, n, f"expected {c} elements, got "
+                            f"{None if t is None else tuple(t.shape)}")
+        out.append(t.to(dtype).contiguous())
+    return out
+
+
 def qkv_epilogue(q, k, v, f: int, h: int, w: int, heads: int, t0: int, norm_q_weight, norm_k_weight,
                  eps: float = 1e-6, theta: float = 10000.0, stream=None):
     """(q', k', v) in window order from the projections q, k, v ((f*h*w, heads*128), natural token order):
     normQ/normK (WanRMSNorm over the full width) + ropeApply at temporal positions t0.. + windowPartition
     (DiT.swift:34-47,100-118,496-506). Returns (q_out, k_out, v_out)."""
     q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
+    c = heads * HEAD_DIM
+    for t, n in ((q2, "q"), (k2, "k"), (v2, "v")):
+        _shaped(t, n, (f * h * w, c), q2.dtype)
+    wq, wk = _norm_weights(norm_q_weight, norm_k_weight, c, q2.dtype)
+    _devices((q2, "q"), (k2, "k"), (v2, "v"), (wq, "norm_q_weight"), (wk, "norm_k_weight"))
     ctx = Context.get(q2.device)
-    wq = _on_device(norm_q_weight.to(q2.dtype).contiguous(), "norm_q_weight", q2.device, q2.shape[1])
-    wk = _on_device(norm_k_weight.to(q2.dtype).contiguous(), "norm_k_weight", q2.device, q2.shape[1])
     tab = rope_tables_device(q2.device, theta)
     qo, ko, vo = torch.empty_like(q2), torch.empty_like(k2), torch.empty_like(v2)
     call("fvsr_qkv_epilogue", ctx.handle, _dtype_code(q2), _ptr(q2), _ptr(k2), _ptr(v2), f, h, w, heads, t0,
@@ -308,6 +401,7 @@ class KVRing:
         self.s = bh * bw
         self.capacity, self.kv_len = capacity, kv_len
         self.dtype = dtype
+        self.channels = heads * HEAD_DIM
         self.code = DTYPE_BF16 if dtype == torch.bfloat16 else DTYPE_F32
         h = C.c_void_p()
         call("fvsr_kv_ring_create", self.ctx.handle, self.code, layers, heads, bh, bw, capacity, kv_len, C.byref(h))
@@ -327,19 +421,34 @@ class KVRing:
     def reset(self):
         call("fvsr_kv_ring_reset", self.handle)
 
+    def _chunk(self, x, name: str, n_slices: int) -> torch.Tensor:
+        """A chunk's token operand: (n_slices * s * 128, C) in the ring's dtype (metadata only)."""
+        x2 = _tokens(x, name)
+        return _shaped(x2, name, (n_slices * self.s * BLOCK, self.channels), self.dtype)
+
+    def _queries(self, x, name: str) -> torch.Tensor:
+        """Queries against this ring: (L, C) in the ring's dtype (the library checks L against the slices)."""
+        x2 = _tokens(x, name)
+        if x2.shape[1] != self.channels or x2.dtype != self.dtype:
+            raise FVSRError(_abi.ERR_INVALID_ARG, name, f"expected (L, {self.channels}) {self.dtype} tokens, got "
+                            f"{tuple(x2.shape)} {x2.dtype}")
+        return x2
+
     def append(self, layer: int, k_new, v_new, n_slices: int, layout: int = LAYOUT_WINDOWS, stream=None):
-        k2, v2 = _tokens(k_new, "k_new"), _tokens(v_new, "v_new")
+        k2, v2 = self._chunk(k_new, "k_new", n_slices), self._chunk(v_new, "v_new", n_slices)
+        _devices((k2, "k_new"), (v2, "v_new"))
         call("fvsr_kv_ring_append", self.handle, layer, _ptr(k2), _ptr(v2), n_slices, layout, _stream(stream))
 
     def append_qkv(self, layer: int, q, k, v, n_slices: int, t0: int, norm_q_weight, norm_k_weight,
                    eps: float = 1e-6, theta: float = 10000.0, stream=None, q_out=None):
         """The projection epilogue straight into the ring (DiT.swift:496-511): appends k' = rope(normK(k)) and v of
         the chunk (natural token order, f = 2 * n_slices) and returns q' = rope(normQ(q)) in window order."""
-        q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
-        wq = norm_q_weight.to(q2.dtype).contiguous()
-        wk = norm_k_weight.to(q2.dtype).contiguous()
+        q2, k2, v2 = (self._chunk(t, n, n_slices) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+        wq, wk = _norm_weights(norm_q_weight, norm_k_weight, self.channels, self.dtype)
+        qo = _out_meta(q_out, q2, "q_out")
+        _devices((q2, "q"), (k2, "k"), (v2, "v"), (wq, "norm_q_weight"), (wk, "norm_k_weight"), (qo, "q_out"))
+        qo = torch.empty_like(q2) if qo is None else qo
         tab = rope_tables_device(q2.device, theta)
-        qo = torch.empty_like(q2) if q_out is None else _tokens(q_out, "q_out")
         call("fvsr_kv_ring_append_qkv", self.handle, layer, _ptr(q2), _ptr(k2), _ptr(v2), n_slices, t0, _ptr(wq),
              _ptr(wk), float(eps), _ptr(tab), _ptr(qo), _stream(stream))
         return qo
@@ -349,19 +458,21 @@ class KVRing:
                        out=None, q_work=None, want_mask=False, want_probs=False):
         """The LCSA layer call from the projections (DiT.swift:496-539): epilogue into the ring, select, attend,
         evict; returns (o in natural token order, mask, probs)."""
-        q2, k2, v2 = _tokens(q, "q"), _tokens(k, "k"), _tokens(v, "v")
-        wq = norm_q_weight.to(q2.dtype).contiguous()
-        wk = norm_k_weight.to(q2.dtype).contiguous()
+        q2, k2, v2 = (self._chunk(t, n, n_new_slices) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+        wq, wk = _norm_weights(norm_q_weight, norm_k_weight, self.channels, self.dtype)
+        qw, o = _out_meta(q_work, q2, "q_work"), _out_meta(out, q2)
+        _devices((q2, "q"), (k2, "k"), (v2, "v"), (wq, "norm_q_weight"), (wk, "norm_k_weight"), (qw, "q_work"),
+                 (o, "out"))
+        qw = torch.empty_like(q2) if qw is None else qw
+        o = torch.empty_like(q2) if o is None else o
         tab = rope_tables_device(q2.device, theta)
-        qw = torch.empty_like(q2) if q_work is None else _tokens(q_work, "q_work")
-        o = torch.empty_like(q2) if out is None else _tokens(out, "out")
         nq = n_new_slices * self.s
         nk = (self.slices(layer) + n_new_slices) * self.s
         dev = q2.device
         mask = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_mask else None
         probs = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
         call("fvsr_lcsa_layer_qkv", self.ctx.handle, self.handle, layer, _ptr(q2), _ptr(k2), _ptr(v2), n_new_slices,
-             t0, _ptr(wq), _ptr(wk), float(eps), _ptr(tab), _ptr(self.ctx.local_device(local)), topk, mode,
+             t0, _ptr(wq), _ptr(wk), float(eps), _ptr(tab), _ptr(self.ctx.local_device(local, self.s)), topk, mode,
              _ptr(qw), _ptr(o), _ptr(mask), _ptr(probs), _stream(stream))
         return o, mask, probs
 
@@ -383,7 +494,8 @@ class KVRing:
         return k, v
 
     def select(self, layer: int, qW, q_slices: int, local, topk: int, stream=None, want_mask=True, want_probs=True):
-        q = _tokens(qW, "qW")
+        q = self._queries(qW, "qW")
+        _devices((q, "qW"))
         nq = -(-q.shape[0] // BLOCK)
         nk = self.slices(layer) * self.s
         dev = q.device
@@ -392,13 +504,17 @@ class KVRing:
         kidx = torch.empty((self.heads, nq, nk), dtype=torch.int32, device=dev)
         kcnt = torch.empty((self.heads, nq), dtype=torch.int32, device=dev)
         call("fvsr_lcsa_select_ring", self.ctx.handle, self.handle, layer, _ptr(q), q.shape[0], q_slices,
-             _ptr(self.ctx.local_device(local)), topk, _ptr(mask), _ptr(probs), _ptr(kidx), _ptr(kcnt),
+             _ptr(self.ctx.local_device(local, self.s)), topk, _ptr(mask), _ptr(probs), _ptr(kidx), _ptr(kcnt),
              _stream(stream))
         return mask, probs, kidx, kcnt
 
     def attention(self, layer: int, q, kidx, kcnt, mode: int = ATTN_KERNEL, stream=None, out=None):
-        q2 = _tokens(q, "q")
-        o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+        q2 = self._queries(q, "q")
+        _lists_meta(kidx, kcnt, self.heads, -(-q2.shape[0] // BLOCK))
+        o = _out_meta(out, q2)
+        _devices((q2, "q"), (kidx, "kidx"), (kcnt, "kcnt"), (o, "out"))
+        kidx, kcnt = kidx.to(torch.int32).contiguous(), kcnt.to(torch.int32).contiguous()
+        o = torch.empty_like(q2) if o is None else o
         call("fvsr_lcsa_attention_ring", self.ctx.handle, self.handle, layer, _ptr(q2), q2.shape[0], _ptr(kidx),
              _ptr(kcnt), kidx.shape[-1], mode, _ptr(o), _stream(stream))
         return o
@@ -407,16 +523,18 @@ class KVRing:
                    mode: int = ATTN_AUTO, layout: int = LAYOUT_WINDOWS, stream=None, out=None, want_mask=False,
                    want_probs=False):
         """append -> select -> attention -> evict: the LCSA core of blockForward (DiT.swift:504-538)."""
-        q2 = _tokens(qW, "qW")
-        k2, v2 = _tokens(k_new, "k_new"), _tokens(v_new, "v_new")
-        o = torch.empty_like(q2) if out is None else _tokens(out, "out")
+        q2 = self._queries(qW, "qW")
+        k2, v2 = self._chunk(k_new, "k_new", n_new_slices), self._chunk(v_new, "v_new", n_new_slices)
+        o = _out_meta(out, q2)
+        _devices((q2, "qW"), (k2, "k_new"), (v2, "v_new"), (o, "out"))
+        o = torch.empty_like(q2) if o is None else o
         nq = -(-q2.shape[0] // BLOCK)
         nk = (self.slices(layer) + n_new_slices) * self.s
         dev = q2.device
         mask = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_mask else None
         probs = torch.empty((self.heads, nq, nk), dtype=torch.float32, device=dev) if want_probs else None
         call("fvsr_lcsa_layer", self.ctx.handle, self.handle, layer, _ptr(q2), q2.shape[0], _ptr(k2), _ptr(v2),
-             n_new_slices, layout, q_slices, _ptr(self.ctx.local_device(local)), topk, mode, _ptr(o), _ptr(mask),
+             n_new_slices, layout, q_slices, _ptr(self.ctx.local_device(local, self.s)), topk, mode, _ptr(o), _ptr(mask),
              _ptr(probs), _stream(stream))
         return o, mask, probs
 
@@ -485,6 +603,9 @@ class DiTBlock:
     def set_context(self, context: torch.Tensor, stream=None):
         """context: (ctx_len, C) bf16 text-embedded prompt -> cached cross K/V."""
         ctxt = _tokens(context.to(torch.bfloat16).contiguous(), "context")
+        _shaped(ctxt, "context", (ctxt.shape[0], self.dim))
+        _devices((ctxt, "context"))
+        _on_device(ctxt, "context", self.device)
         n = ctxt.shape[0]
         self.t["cross_k"] = torch.empty_like(ctxt)
         self.t["cross_v"] = torch.empty_like(ctxt)
@@ -498,13 +619,20 @@ class DiTBlock:
     def forward(self, ring: "KVRing", layer: int, x: torch.Tensor, t_mod: torch.Tensor, n_new_slices: int, t0: int,
                 local, topk: int, mode: int = ATTN_AUTO, theta: float = 10000.0, stream=None) -> torch.Tensor:
         """x: (L, C) bf16 tokens in natural (f, h, w) order, updated in place and returned; t_mod: (6, C)."""
+        if ring.dtype != torch.bfloat16 or ring.channels != self.dim:
+            raise FVSRError(_abi.ERR_INVALID_ARG, "ring", f"expected a bf16 ring of {self.dim} channels, got "
+                            f"{ring.dtype} with {ring.channels}")
         x2 = _tokens(x, "x")
         if x2.dtype != torch.bfloat16:
             raise FVSRError(_abi.ERR_UNSUPPORTED, "DiTBlock.forward", "bf16 tokens only")
-        _on_device(x2, "x", self.device, x2.shape[0] * self.dim)
-        tm = _on_device(t_mod.to(torch.bfloat16).reshape(6, -1).contiguous(), "t_mod", self.device, 6 * self.dim)
+        _shaped(x2, "x", (n_new_slices * ring.s * BLOCK, self.dim))
+        if t_mod.numel() != 6 * self.dim:
+            raise FVSRError(_abi.ERR_INVALID_ARG, "t_mod", f"expected (6, {self.dim}), got {tuple(t_mod.shape)}")
+        tm = t_mod.to(torch.bfloat16).reshape(6, -1).contiguous()
+        _devices((x2, "x"), (tm, "t_mod"))
+        _on_device(x2, "x", self.device)
         tab = rope_tables_device(x2.device, theta)
         w = self._struct()
         call("fvsr_dit_block", ring.ctx.handle, ring.handle, layer, C.byref(w), _ptr(tm), _ptr(x2), n_new_slices, t0,
-             float(self.eps), _ptr(tab), _ptr(ring.ctx.local_device(local)), topk, mode, _stream(stream))
+             float(self.eps), _ptr(tab), _ptr(ring.ctx.local_device(local, ring.s)), topk, mode, _stream(stream))
         return x

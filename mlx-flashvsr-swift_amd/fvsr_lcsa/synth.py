@@ -37,6 +37,8 @@ class Workload:
     smooth: bool = False        # low-frequency field + noise: pooled scores with distinct margins
     full_mask: bool = False     # every block kept (sparse == dense)
     q_t0: int = 0               # temporal RoPE position of the first query frame
+    seed: int = 0               # default generator seed
+    noise: float = 0.35         # noise std of the smooth workloads (per element, before the RMS norm)
     description: str = ""
 
     @property
@@ -100,13 +102,20 @@ WORKLOADS = {
         description="1280x768, bf16: Lq 7680, Lk 19200 (5 frames), all blocks kept (sparse == dense)"),
     "sparse_1280x768_bf16": Workload(
         "sparse_1280x768_bf16", 768, 1280, q_frames=2, k_frames=5, dtype=torch.bfloat16, local_range=3,
-        kept_fraction=0.6, smooth=True, q_t0=3,
-        description="1280x768, bf16: Lq 7680, Lk 19200, local range 3, 60% of in-window kept, smooth Q/K + noise"),
+        kept_fraction=0.6, smooth=True, q_t0=3, seed=1,
+        description="1280x768, bf16: Lq 7680, Lk 19200, local range 3, 60% of in-window kept, smooth Q/K + noise; "
+                    "seed 1 puts every top-k threshold 2.2e-3 (relative) below its upper neighbour"),
     "sparse_1920x1152_bf16": Workload(
         "sparse_1920x1152_bf16", 1152, 1920, q_frames=2, k_frames=5, dtype=torch.bfloat16, local_range=11,
-        kept_fraction=0.3, rope=True, q_t0=3,
+        kept_fraction=0.3, rope=True, smooth=True, noise=1.0, q_t0=3, seed=0,
         description="1920x1152, bf16: Lq 17280, Lk 43200 (337.5 key blocks, ragged tail), local range 11, "
-                    "30% of in-window kept, per-head RMS norm + 3-D RoPE"),
+                    "30% of in-window kept, smooth Q/K field + N(0,1) noise, per-head RMS norm + 3-D RoPE; seed 0 "
+                    "puts every top-k threshold 8.7e-5 (relative) below its upper neighbour"),
+    "sparse_1920x1152_bf16_iid": Workload(
+        "sparse_1920x1152_bf16_iid", 1152, 1920, q_frames=2, k_frames=5, dtype=torch.bfloat16, local_range=11,
+        kept_fraction=0.3, rope=True, q_t0=3,
+        description="1920x1152, bf16: as sparse_1920x1152_bf16 with i.i.d. N(0,1) Q/K (pooled blocks carry no "
+                    "signal: the mask follows the window sizes and 960 of 1620 rows select nothing)"),
 }
 
 
@@ -187,11 +196,14 @@ def smooth_field(f: int, h: int, w: int, channels: int, gen: torch.Generator, mo
 # ----------------------------------------------------------------------------------------------------------------
 # workloads
 # ----------------------------------------------------------------------------------------------------------------
-def make_qkv(wl: Workload, seed: int = 0, device="cpu", noise: float = 0.35):
+def make_qkv(wl: Workload, seed: int | None = None, device="cpu", noise: float | None = None):
     """Seeded (q, k, v) for a workload: q (Lq, C), k/v (Lk, C) in window order, `wl.dtype`, on `device`.
+    `seed` and `noise` default to the workload's own.
 
     Generation happens on the CPU with a torch.Generator (deterministic across machines) in float32, then the
     tensors are cast and moved."""
+    seed = wl.seed if seed is None else seed
+    noise = wl.noise if noise is None else noise
     gen = torch.Generator().manual_seed(seed)
     c, H = wl.channels, wl.heads
     h, w = wl.lat_h, wl.lat_w

@@ -124,6 +124,119 @@ def test_binding_rejects_host_operands_before_any_device_call():
     with pytest.raises(fvsr_lcsa.FVSRError, match="expected a tensor on") as ei:
         fvsr_lcsa.linear(x, w)
     assert ei.value.status == _abi.ERR_INVALID_ARG
-    with pytest.raises(fvsr_lcsa.FVSRError, match="device tensor"):
-        fvsr_lcsa.block_sparse_attention(x, x, x, torch.zeros((1, 1, 1), dtype=torch.int32),
+    t = torch.zeros((4, 128), dtype=torch.bfloat16)
+    with pytest.raises(fvsr_lcsa.FVSRError, match="HIP device"):
+        fvsr_lcsa.block_sparse_attention(t, t, t, torch.zeros((1, 1, 1), dtype=torch.int32),
                                          torch.zeros((1, 1), dtype=torch.int32), 1)
+
+
+def _host_ring(heads=2, bh=2, bw=3, dtype=None):
+    """A KVRing shell with the geometry of a real one but no library handle: enough for the binding's argument
+    checks, which all run before any library call (so no GPU is needed)."""
+    import torch
+    r = object.__new__(fvsr_lcsa.KVRing)
+    r.ctx, r.handle = None, None
+    r.layers, r.heads, r.bh, r.bw, r.s = 1, heads, bh, bw, bh * bw
+    r.capacity, r.kv_len = 4, 3
+    r.dtype = torch.bfloat16 if dtype is None else dtype
+    r.channels = heads * 128
+    r.code = _abi.DTYPE_BF16
+    return r
+
+
+def test_binding_rejects_wrong_extents_before_any_device_call():
+    """Every operand whose extent the library derives from other arguments is checked for shape and dtype before
+    its device, so a short list, a narrow token buffer, a wrong-sized output or an int64 list is named on the host
+    (the C ABI sees only pointers and would read or write past the buffer)."""
+    import torch
+    E = fvsr_lcsa.FVSRError
+    bf = torch.bfloat16
+    q = torch.zeros((256, 256), dtype=bf)
+    k = torch.zeros((384, 256), dtype=bf)
+    kidx = torch.zeros((2, 2, 3), dtype=torch.int32)
+    kcnt = torch.zeros((2, 2), dtype=torch.int32)
+    # attention from lists
+    with pytest.raises(E, match="expected \\(L, 384\\)"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt, 3)              # width is not heads * 128
+    with pytest.raises(E, match="kidx"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx[:, :1], kcnt, 2)       # lists of one query block, two needed
+    with pytest.raises(E, match="kcnt"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt[:1], 2)
+    with pytest.raises(E, match="integer"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx.float(), kcnt, 2)
+    with pytest.raises(E, match="shape of k"):
+        fvsr_lcsa.block_sparse_attention(q, k, k[:128], kidx, kcnt, 2)
+    with pytest.raises(E, match="out"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt, 2, out=torch.zeros((128, 256), dtype=bf))
+    with pytest.raises(E, match="out"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt, 2, out=torch.zeros((256, 256)))   # fp32 out
+    with pytest.raises(E, match="HIP device"):
+        fvsr_lcsa.block_sparse_attention(q, k, k, kidx.long(), kcnt, 2)       # right shapes: only the device is wrong
+    # attention under a mask
+    with pytest.raises(E, match="block_mask"):
+        fvsr_lcsa.kernel_block_attention(q, k, k, torch.ones((2, 2, 2)), 2)   # 3 key blocks
+    with pytest.raises(E, match="out"):
+        fvsr_lcsa.block_masked_attention(q, k, k, torch.ones((2, 2, 3)), 2, out=torch.zeros((256, 128), dtype=bf))
+    # selection
+    with pytest.raises(E, match="qW"):
+        fvsr_lcsa.draft_block_mask_and_probs(q, k, 1, 1, 2, np.ones((2, 2), bool), 1)
+    with pytest.raises(E, match="kW"):
+        fvsr_lcsa.draft_block_mask_and_probs(q, k.float(), 2, 1, 2, np.ones((2, 2), bool), 1)
+    # epilogue
+    w = torch.ones(256, dtype=bf)
+    with pytest.raises(E, match="norm_k_weight"):
+        fvsr_lcsa.qkv_epilogue(q[:128], q[:128], q[:128], 2, 8, 8, 2, 0, w, w[:128])
+    with pytest.raises(E, match="'k'|k:|expected shape"):
+        fvsr_lcsa.qkv_epilogue(q[:128], q[:64], q[:128], 2, 8, 8, 2, 0, w, w)
+
+
+def test_ring_binding_rejects_wrong_extents_before_any_device_call():
+    import torch
+    E = fvsr_lcsa.FVSRError
+    bf = torch.bfloat16
+    ring = _host_ring(heads=2, bh=2, bw=3)        # s = 6 blocks per slice, C = 256
+    tok = torch.zeros((6 * 128, 256), dtype=bf)   # one slice
+    w = torch.ones(256, dtype=bf)
+    local = np.ones((6, 6), bool)
+    with pytest.raises(E, match="k_new"):
+        ring.append(0, tok[:640], tok, 1)
+    with pytest.raises(E, match="v_new"):
+        ring.append(0, tok, tok.float(), 1)                                   # dtype differs from the ring's
+    with pytest.raises(E, match="expected shape"):
+        ring.append(0, tok, tok, 2)                                           # two slices announced, one given
+    with pytest.raises(E, match="norm_q_weight"):
+        ring.append_qkv(0, tok, tok, tok, 1, 0, w[:255], w)
+    with pytest.raises(E, match="q_out"):
+        ring.append_qkv(0, tok, tok, tok, 1, 0, w, w, q_out=tok[:128])
+    with pytest.raises(E, match="q_work"):
+        ring.layer_call_qkv(0, tok, tok, tok, 1, 0, w, w, local, 10, q_work=tok[:, :128])
+    with pytest.raises(E, match="out"):
+        ring.layer_call_qkv(0, tok, tok, tok, 1, 0, w, w, local, 10, out=tok.float())
+    with pytest.raises(E, match="kidx"):
+        ring.attention(0, tok, torch.zeros((2, 5, 4), dtype=torch.int32), torch.zeros((2, 6), dtype=torch.int32))
+    with pytest.raises(E, match="kcnt"):
+        ring.attention(0, tok, torch.zeros((2, 6, 4), dtype=torch.int32), torch.zeros((2, 5), dtype=torch.int32))
+    with pytest.raises(E, match="qW"):
+        ring.select(0, torch.zeros((768, 384), dtype=bf), 1, local, 10)
+    with pytest.raises(E, match="k_new"):
+        ring.layer_call(0, tok, tok[:128], tok, 1, 1, local, 10)
+    with pytest.raises(E, match="HIP device"):
+        ring.layer_call(0, tok, tok, tok, 1, 1, local, 10)                    # right shapes, host tensors
+
+
+def test_dit_block_forward_checks_ring_and_tokens():
+    import torch
+    E = fvsr_lcsa.FVSRError
+    blk = object.__new__(fvsr_lcsa.DiTBlock)
+    blk.dim, blk.heads, blk.device = 256, 2, torch.device("cuda:0")
+    ring = _host_ring(heads=2, bh=2, bw=3)
+    x = torch.zeros((6 * 128, 256), dtype=torch.bfloat16)
+    tm = torch.zeros((6, 256), dtype=torch.bfloat16)
+    with pytest.raises(E, match="expected shape"):
+        blk.forward(ring, 0, x[:512], tm, 1, 0, np.ones((6, 6), bool), 10)     # rows are not one slice
+    with pytest.raises(E, match="ring"):
+        blk.forward(_host_ring(heads=3, bh=2, bw=3), 0, x, tm, 1, 0, np.ones((6, 6), bool), 10)
+    with pytest.raises(E, match="t_mod"):
+        blk.forward(ring, 0, x, tm[:5], 1, 0, np.ones((6, 6), bool), 10)
+    with pytest.raises(E, match="HIP device"):
+        blk.forward(ring, 0, x, tm, 1, 0, np.ones((6, 6), bool), 10)

@@ -215,23 +215,82 @@ def test_c2_full_mask_sparse_equals_dense_bf16(dev):
     assert rel <= BF16_REL
 
 
+def _rows_vs_oracle(q, k, v, mask_np, heads, o, pairs):
+    """Worst rel of the GPU output against the float64 oracle over the listed (head, query block) rows."""
+    qn, kn, vn = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    got = _np(o)
+    worst = 0.0
+    for h, b in pairs:
+        ref = O.block_masked_attention(qn, kn, vn, mask_np, heads, heads_subset=[h], qblocks_subset=[b])
+        r = slice(b * 128, min((b + 1) * 128, got.shape[0]))
+        c = slice(h * 128, (h + 1) * 128)
+        worst = max(worst, O.compare(got[r, c], ref[r, c])["rel"])
+    return worst
+
+
 def test_c4_bf16_subset_vs_oracle(dev):
-    """1920x1152 bf16 (Lq 17280, Lk 43200 with a ragged last key block), mask from the GPU selection; a subset of
-    (head, query block) rows against the float64 oracle at rel <= 1e-2, and kernel == dense fallback everywhere."""
+    """1920x1152 bf16 (Lq 17280, Lk 43200 with a ragged last key block), the oracle's block mask (equal to the
+    GPU selection's, which test_gpu_select checks bit for bit): three query blocks of every head against the float64
+    oracle at rel <= 1e-2 (each row non-empty, lists of different lengths), kernel == dense fallback everywhere."""
     wl = synth.WORKLOADS["sparse_1920x1152_bf16"]
-    q, k, v = synth.make_qkv(wl, seed=0)
+    q, k, v = synth.make_qkv(wl)
+    local = synth.local_mask(wl).numpy()
+    topk = synth.workload_topk(wl)
+    mask_np, _ = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads, wl.q_slices, wl.s,
+                                              local, topk, lk=wl.lk)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    md = torch.from_numpy(mask_np).to(dev)
+    o = fvsr_lcsa.kernel_block_attention(qd, kd, vd, md, wl.heads)
+    od = fvsr_lcsa.block_masked_attention(qd, kd, vd, md, wl.heads)
+    assert torch.equal(o, od)
+    assert torch.isfinite(o.float()).all()
+    # per head: the query blocks with the shortest and the longest list, and one in the middle of the grid
+    kc = mask_np.sum(-1)
+    pairs = []
+    for h in range(wl.heads):
+        for b in {int(kc[h].argmin()), int(kc[h].argmax()), (11 * h + 67) % wl.nq}:
+            assert kc[h, b] > 0
+            pairs.append((h, b))
+    assert _rows_vs_oracle(q, k, v, mask_np, wl.heads, o, pairs) <= BF16_REL
+
+
+def test_c3_bf16_attention_vs_oracle(dev):
+    """1280x768 bf16 block-sparse (local range 3, 60% of in-window pairs; tie-free smooth Q/K at the workload's
+    seed), the oracle's own mask: two query blocks of every head against the float64 oracle at rel <= 1e-2
+    (DiT.swift:279-313), kernel == dense fallback everywhere."""
+    wl = synth.WORKLOADS["sparse_1280x768_bf16"]
+    q, k, v = synth.make_qkv(wl)
+    local = synth.local_mask(wl).numpy()
+    topk = synth.workload_topk(wl)
+    mask_np, probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads, wl.q_slices, wl.s,
+                                                  local, topk)
+    assert O.threshold_margin(probs, wl.q_slices, topk) >= 1e-3
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    md = torch.from_numpy(mask_np).to(dev)
+    o = fvsr_lcsa.kernel_block_attention(qd, kd, vd, md, wl.heads)
+    od = fvsr_lcsa.block_masked_attention(qd, kd, vd, md, wl.heads)
+    assert torch.equal(o, od)
+    pairs = [(h, b) for h in range(wl.heads) for b in ((7 * h) % wl.nq, (7 * h + 31) % wl.nq)]
+    assert _rows_vs_oracle(q, k, v, mask_np, wl.heads, o, pairs) <= BF16_REL
+
+
+def test_c4_iid_workload_subset(dev):
+    """The i.i.d. 1920x1152 workload (960 of 1620 rows select nothing): empty rows are zeros, non-empty rows match
+    the oracle, kernel == dense fallback."""
+    wl = synth.WORKLOADS["sparse_1920x1152_bf16_iid"]
+    q, k, v = synth.make_qkv(wl)
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     local = synth.local_mask(wl).numpy()
-    mask, _, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(qd, kd, wl.heads, wl.q_slices, wl.s, local,
-                                                               synth.workload_topk(wl), want_probs=False)
+    mask, _, _, kcnt = fvsr_lcsa.draft_block_mask_and_probs(qd, kd, wl.heads, wl.q_slices, wl.s, local,
+                                                            synth.workload_topk(wl), want_probs=False)
     o = fvsr_lcsa.kernel_block_attention(qd, kd, vd, mask, wl.heads)
     od = fvsr_lcsa.block_masked_attention(qd, kd, vd, mask, wl.heads)
     assert torch.equal(o, od)
-    heads_sel, qb_sel = [0, 5, 11], [0, 67, 134]
-    ref = O.block_masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask.cpu().numpy(),
-                                   wl.heads, heads_subset=heads_sel, qblocks_subset=qb_sel)
-    got = _np(o)
-    rows = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in qb_sel])
-    cols = np.concatenate([np.arange(h * 128, h * 128 + 128) for h in heads_sel])
-    assert O.compare(got[np.ix_(rows, cols)], ref[np.ix_(rows, cols)])["rel"] <= BF16_REL
-    assert torch.isfinite(o.float()).all()
+    kc = kcnt.cpu().numpy()
+    ov = o.float().cpu().view(wl.nq, 128, wl.heads, 128)
+    empty = np.argwhere(kc == 0)
+    assert len(empty) > 0
+    for h, b in empty[:: max(1, len(empty) // 16)]:
+        assert (ov[b, :, h] == 0).all()
+    full = [tuple(x) for x in np.argwhere(kc > 0)[:: max(1, int((kc > 0).sum()) // 12)]]
+    assert _rows_vs_oracle(q, k, v, mask.cpu().numpy(), wl.heads, o, full) <= BF16_REL

@@ -87,19 +87,15 @@ def test_c1_select(dev, seed):
 
 
 def test_c3_select_tie_free_is_bit_exact(dev):
-    """1280x768 bf16 with a smooth field + noise: pick the first seed whose every top-k row has a margin >= 1e-3
-    (the BASELINE 'no ties within 1e-3' condition) and require the GPU mask to equal the oracle's bit for bit."""
+    """1280x768 bf16 with a smooth field + noise, at the workload's seed: every top-k row has a margin >= 1e-3 (the
+    BASELINE 'no ties within 1e-3' condition), and the GPU mask must equal the oracle's bit for bit."""
     wl = synth.WORKLOADS["sparse_1280x768_bf16"]
     local = synth.local_mask(wl).numpy()
     topk = synth.workload_topk(wl)
-    for seed in range(12):
-        q, k, _ = synth.make_qkv(wl, seed=seed)
-        ref_mask, ref_probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads,
-                                                           wl.q_slices, wl.s, local, topk)
-        if O.threshold_margin(ref_probs, wl.q_slices, topk) >= 1e-3:
-            break
-    else:
-        pytest.fail("no tie-free seed in 12 draws")
+    q, k, _ = synth.make_qkv(wl)
+    ref_mask, ref_probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads,
+                                                       wl.q_slices, wl.s, local, topk)
+    assert O.threshold_margin(ref_probs, wl.q_slices, topk) >= 1e-3
     mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q.to(dev), k.to(dev), wl.heads, wl.q_slices,
                                                                    wl.s, local, topk)
     np.testing.assert_array_equal(mask.cpu().numpy(), ref_mask)
@@ -107,17 +103,61 @@ def test_c3_select_tie_free_is_bit_exact(dev):
     check_lists(mask, kidx, kcnt)
 
 
-def test_c4_select_ragged(dev):
-    """1920x1152 bf16: Lk 43200 = 337.5 key blocks (the last pooled over its 64 valid tokens), local 11."""
+C4_MARGIN = 5e-5   # relative gap at every top-k threshold of the 1920x1152 workload (~400 fp32 ulps)
+
+
+def near_threshold_rel(got, ref, q_slices, topk):
+    """Largest per-element relative difference of the probabilities over the entries within a factor 2 of their
+    (head, slice) row's top-k threshold: the entries whose order decides the mask."""
+    h, nq, nk = ref.shape
+    g = got.reshape(h * q_slices, -1).astype(np.float64)
+    r = ref.reshape(h * q_slices, -1).astype(np.float64)
+    n = r.shape[1]
+    thr = np.sort(r, axis=1)[:, n - 1 - min(n - 1, topk)][:, None]
+    near = (r >= thr / 2) & (r <= thr * 2) & (r > 0)
+    return float((np.abs(g - r)[near] / r[near]).max())
+
+
+def test_c4_select_tie_free_is_bit_exact(dev):
+    """1920x1152 bf16 (Lk 43200 = 337.5 key blocks, the last pooled over its 64 valid tokens, local 11, 30% of the
+    in-window pairs): Q/K a smooth field + noise with RMS norm and 3-D RoPE, at the workload's seed. Every (head,
+    slice) threshold is >= 5e-5 (relative) from its upper neighbour, far above the measured per-element difference of
+    the probabilities, and the GPU mask must equal the oracle's bit for bit (DiT.swift:158-174). The mask is not
+    degenerate: rows differ between heads and fewer than 10 % select nothing."""
     wl = synth.WORKLOADS["sparse_1920x1152_bf16"]
-    q, k, _ = synth.make_qkv(wl, seed=0)
+    q, k, _ = synth.make_qkv(wl)
+    local = synth.local_mask(wl).numpy()
+    topk = synth.workload_topk(wl)
+    ref_mask, ref_probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads,
+                                                       wl.q_slices, wl.s, local, topk, lk=wl.lk)
+    margin = O.threshold_margin(ref_probs, wl.q_slices, topk)
+    assert margin >= C4_MARGIN
+    mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q.to(dev), k.to(dev), wl.heads, wl.q_slices,
+                                                                   wl.s, local, topk)
+    assert mask.shape == (wl.heads, 135, 338)
+    rel_elem = near_threshold_rel(probs.cpu().numpy(), ref_probs, wl.q_slices, topk)
+    print(f"  threshold margin {margin:.3e}, probs rel diff near the thresholds {rel_elem:.3e}", flush=True)
+    assert rel_elem <= margin / 8
+    np.testing.assert_array_equal(mask.cpu().numpy(), ref_mask)
+    kc = kcnt.cpu().numpy()
+    assert (kc.reshape(wl.heads * wl.q_slices, -1).sum(1) == topk).all()
+    assert (kc == 0).mean() < 0.1
+    assert any(not np.array_equal(kc[0], kc[h]) for h in range(1, wl.heads))
+    check_lists(mask, kidx, kcnt)
+
+
+def test_c4_iid_select_near_ties(dev):
+    """The same geometry with i.i.d. N(0,1) Q/K: pooling 128 independent tokens leaves no signal, so the
+    probabilities of a row cluster within a few ulps and the threshold margin is ~1e-6. The mask must equal the
+    oracle's except at near-ties, where any flip must satisfy the reference's near-tie rule (Gates.swift:239-277)."""
+    wl = synth.WORKLOADS["sparse_1920x1152_bf16_iid"]
+    q, k, _ = synth.make_qkv(wl)
     local = synth.local_mask(wl).numpy()
     topk = synth.workload_topk(wl)
     ref_mask, ref_probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads,
                                                        wl.q_slices, wl.s, local, topk, lk=wl.lk)
     mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q.to(dev), k.to(dev), wl.heads, wl.q_slices,
                                                                    wl.s, local, topk)
-    assert mask.shape == (wl.heads, 135, 338)
     assert O.compare(probs.cpu().numpy(), ref_probs)["rel"] <= 1e-5
     check_mask(mask, ref_mask, ref_probs, wl.q_slices, topk)
     check_lists(mask, kidx, kcnt)
@@ -138,7 +178,7 @@ def test_threshold_bin_paths_1920x1152_local3(dev, topk):
     """1920x1152 geometry with local range 3: ~94 % of each (head, slice) row of 45630 probs are exact zeros. topk
     2000 puts the threshold among the nonzero probs (the histogram bin is gathered in LDS); topk 44000 puts it on
     the zeros, a bin far larger than the LDS candidate buffer, so the full-row radix select runs."""
-    wl = synth.WORKLOADS["sparse_1920x1152_bf16"]
+    wl = synth.WORKLOADS["sparse_1920x1152_bf16_iid"]
     q, k, _ = synth.make_qkv(wl, seed=1)
     local = O.local_block_mask(wl.bh, wl.bw, 3)
     ref_mask, ref_probs = O.draft_block_mask_and_probs(q.float().numpy(), k.float().numpy(), wl.heads,
