@@ -129,9 +129,9 @@ def test_list_and_mask_operands_are_checked(dev):
     kidx = torch.zeros((heads, 2, 3), dtype=torch.int32, device=dev)
     kcnt = torch.zeros((heads, 2), dtype=torch.int32, device=dev)
     fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt, heads)          # the right shapes run
-    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+    with pytest.raises(fvsr_lcsa.FVSRError, match="kidx"):
         fvsr_lcsa.block_sparse_attention(q, k, k, kidx[:, :1], kcnt, heads)   # lists of one query block, two needed
-    with pytest.raises(fvsr_lcsa.FVSRError, match="elements"):
+    with pytest.raises(fvsr_lcsa.FVSRError, match="kcnt"):
         fvsr_lcsa.block_sparse_attention(q, k, k, kidx, kcnt[:1], heads)
     with pytest.raises(fvsr_lcsa.FVSRError, match="expected a tensor on"):
         fvsr_lcsa.block_sparse_attention(q, k, k, kidx.cpu(), kcnt, heads)
