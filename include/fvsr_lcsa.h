@@ -104,6 +104,17 @@ int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, con
                         int64_t lk, int heads, const int32_t* kidx, const int32_t* kcnt, int nk_stride, void* o,
                         void* stream);
 
+/* No counterpart in the reference: fvsr_lcsa_attention for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and results as
+ * fvsr_lcsa_attention; the persistent walk's row order and work counter live in a static device array of the
+ * library (1 MiB + 256 B per GPU, held until the process ends) instead of the context workspace, so the call
+ * allocates nothing. heads * ceil(lq / 128) must be <= 262144 (FVSR_ERR_UNSUPPORTED otherwise, before any device
+ * work). The context must exist (fvsr_ctx_create takes the array's device address). Calls that overlap on one GPU
+ * share the array and race: serialise them (one stream, or events). */
+int fvsr_lcsa_attention_noalloc(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
+                                int64_t lk, int heads, const int32_t* kidx, const int32_t* kcnt, int nk_stride,
+                                void* o, void* stream);
+
 /* Replaces `FlashVSRAttentionOps.kernel` / `.dense` (SparseAttention.swift:190-202): attention under a block mask
  * (H, Nq, Nk) f32 tested > 0.5. mode FVSR_ATTN_KERNEL visits only the selected blocks; FVSR_ATTN_DENSE is the
  * dense fallback of `blockMaskedAttention` (DiT.swift:279-313): the same kernel walks EVERY key block and masks the

@@ -47,6 +47,8 @@ int launch_residual_norm(void* x, const void* y, const void* gate, int64_t L, in
                          const void* bias, const void* scale, const void* shift, void* out, hipStream_t stream);
 int launch_rms_norm(const void* x, int64_t L, int C, float eps, const void* w, void* out, hipStream_t stream);
 int launch_full_lists(int rows, int nkc, int32_t* kidx, int32_t* kcnt, hipStream_t stream);
+int noalloc_scratch_init(int device);
+int noalloc_scratch(int device, int64_t rows, int32_t** order, int32_t** counter);
 void rope_tables_host(double theta, float* out);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
                        int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
@@ -164,6 +166,14 @@ int fvsr_ctx_create(int device, fvsr_ctx** out) {
   int n = 0;
   FVSR_HIP_CHECK(hipGetDeviceCount(&n));
   FVSR_REQUIRE(device >= 0 && device < n, FVSR_ERR_INVALID_ARG, "no such device");
+  // the device address of the allocation-free entry point's static scratch, taken once per device with the
+  // device current
+  int prev = 0;
+  FVSR_HIP_CHECK(hipGetDevice(&prev));
+  FVSR_HIP_CHECK(hipSetDevice(device));
+  const int rc = noalloc_scratch_init(device);
+  FVSR_HIP_CHECK(hipSetDevice(prev));
+  if (rc) return rc;
   fvsr_ctx* c = new (std::nothrow) fvsr_ctx();
   FVSR_REQUIRE(c != nullptr, FVSR_ERR_OUT_OF_MEMORY, "context allocation failed");
   c->device = device;
@@ -342,6 +352,20 @@ int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, con
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o);
   if ((rc = attach_order(ctx, a, nk))) return rc;
+  return launch_attention(dtype, false, a, (hipStream_t)stream);
+}
+
+int fvsr_lcsa_attention_noalloc(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
+                                int64_t lk, int heads, const int32_t* kidx, const int32_t* kcnt, int nk_stride,
+                                void* o, void* stream) {
+  int rc = check_attn_common(ctx, dtype, q, lq, k, v, lk, heads, o);
+  if (rc) return rc;
+  FVSR_REQUIRE(kidx && kcnt, FVSR_ERR_INVALID_ARG, "kidx and kcnt must be non-NULL");
+  FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
+  const int nk = (int)ceil_div(lk, kBlock);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o);
+  if ((rc = noalloc_scratch(ctx->device, (int64_t)heads * a.nq, &a.order, &a.counter))) return rc;
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   return launch_attention(dtype, false, a, (hipStream_t)stream);
 }
 

@@ -21,6 +21,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBlock = 128;     // tokens per LCSA window / block
 constexpr int kHeadDim = 128;   // head dim of every FlashVSR head
 constexpr int kXcds = 8;        // MI355X: 8 XCDs, workgroups dispatched round-robin across them
+constexpr int kMaxDevices = 64; // device indices with per-device state (scratch addresses, CU counts)
 constexpr int kPoolParts = 4;   // a block mean is summed as 4 runs of 32 tokens, then ((p0 + p1) + (p2 + p3)) / n
 
 // Records the failure message for fvsr_last_error() and returns the status (defined in api.hip).

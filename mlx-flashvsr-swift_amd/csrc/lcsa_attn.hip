@@ -12,6 +12,7 @@
 // contiguous run of (head, query block) items.
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -970,6 +971,55 @@ int launch_attention(int dtype, bool dense, const AttnArgs& a, hipStream_t strea
     else hipLaunchKernelGGL(attn_f32_kernel<false>, grid, block, 0, stream, a);
   }
   FVSR_HIP_CHECK(hipGetLastError());
+  return FVSR_OK;
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// allocation-free scratch of fvsr_lcsa_attention_noalloc
+// ------------------------------------------------------------------------------------------------------------
+// The persistent walk's row order (one int32 per (head, query block) row) and its work counter live in a file-scope
+// device array instead of the context workspace: bytes [0, 256) hold the counter, the order starts at byte 256.
+// Every GPU holds its own copy for the life of the process. In host code `scratch` names a host-side stand-in, so
+// the device address is taken once per device with hipGetSymbolAddress (noalloc_scratch_init, called by
+// fvsr_ctx_create with the device current) and only that address reaches kernels. The order kernel rewrites the
+// counter and every order entry it uses on each call, so nothing needs clearing; calls that overlap on one GPU
+// share the array and race.
+constexpr int kNoAllocRows = 1 << 18;
+constexpr size_t kNoAllocScratchBytes = 256 + (size_t)kNoAllocRows * sizeof(int32_t);
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+int noalloc_max_rows() { return kNoAllocRows; }
+
+int noalloc_scratch_init(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(FVSR_ERR_UNSUPPORTED, "device index beyond " + std::to_string(kMaxDevices));
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device]) return FVSR_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr)
+    return set_error(FVSR_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  g_scratch_ptr[device] = p;
+  return FVSR_OK;
+}
+
+// the row order and counter of `device`'s scratch for `rows` rows (FVSR_ERR_STATE before noalloc_scratch_init)
+int noalloc_scratch(int device, int64_t rows, int32_t** order, int32_t** counter) {
+  if (rows > kNoAllocRows)
+    return set_error(FVSR_ERR_UNSUPPORTED, "fvsr_lcsa_attention_noalloc: " + std::to_string(rows) +
+                                               " (head, query block) rows exceed its static scratch of " +
+                                               std::to_string(kNoAllocRows));
+  void* p = nullptr;
+  if (device >= 0 && device < kMaxDevices) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[device];
+  }
+  if (!p) return set_error(FVSR_ERR_STATE, "no scratch address for this device: create its context first");
+  *counter = (int32_t*)p;
+  *order = (int32_t*)((char*)p + 256);
   return FVSR_OK;
 }
 

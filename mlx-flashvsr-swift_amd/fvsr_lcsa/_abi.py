@@ -31,6 +31,7 @@ SIGNATURES = {
     "fvsr_attention_mode_auto": (_i, [_i, _i, _i, C.c_double, C.POINTER(C.c_double), C.POINTER(_i)]),
     "fvsr_lcsa_select": (_i, [_vp, _i, _vp, _i64, _vp, _i64, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "fvsr_lcsa_attention": (_i, [_vp, _i, _vp, _i64, _vp, _vp, _i64, _i, _vp, _vp, _i, _vp, _vp]),
+    "fvsr_lcsa_attention_noalloc": (_i, [_vp, _i, _vp, _i64, _vp, _vp, _i64, _i, _vp, _vp, _i, _vp, _vp]),
     "fvsr_lcsa_attention_mask": (_i, [_vp, _i, _vp, _i64, _vp, _vp, _i64, _i, _vp, _i, _vp, _vp]),
     "fvsr_kv_ring_create": (_i, [_vp, _i, _i, _i, _i, _i, _i, _i, C.POINTER(_vp)]),
     "fvsr_kv_ring_destroy": (_i, [_vp]),
