@@ -33,8 +33,8 @@ PROFILE_PMC = os.path.join(ROOT, "profiles", "lcsa_attn_bf16_1920x1152_pmc.txt")
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="sparse_1920x1152_bf16")
     ap.add_argument("--seed", type=int, default=None, help="generator seed (default: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
@@ -521,30 +521,38 @@ def main():
         attend(ki, kc)
     torch.cuda.synchronize()
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # the layer call: K back to back (events only around the loop: an event between two kernels stalls the queue for
+    # several microseconds)
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_start.record(stream)
-    for i in range(args.steps):
+    for _ in range(args.steps):
         if args.attn_only:
-            a0, a1 = ev[i]
-            a0.record(stream)
             attend(kidx, kcnt)
-            a1.record(stream)
             continue
         _, _, ki, kc = select()
-        a0, a1 = ev[i]
-        a0.record(stream)
         attend(ki, kc)
-        a1.record(stream)
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_step = t_start.elapsed_time(t_end) / args.steps
-    ms_attn = sum(a.elapsed_time(b) for a, b in ev) / args.steps
-    ms_select = ms_step - ms_attn
+    # the attention alone (row order + sparse walk, the roofline kernel) and the selection alone, K back to back each,
+    # on the launch stream
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(args.steps):
+        attend(kidx, kcnt)
+    a1.record(stream)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(args.steps):
+        select()
+    s1.record(stream)
+    torch.cuda.synchronize()
+    ms_attn = a0.elapsed_time(a1) / args.steps
+    ms_select = s0.elapsed_time(s1) / args.steps
 
     def timed(fn, n):
         for _ in range(2):

@@ -22,6 +22,10 @@ constexpr int kBlock = 128;     // tokens per LCSA window / block
 constexpr int kHeadDim = 128;   // head dim of every FlashVSR head
 constexpr int kXcds = 8;        // MI355X: 8 XCDs, workgroups dispatched round-robin across them
 constexpr int kMaxDevices = 64; // device indices with per-device state (scratch addresses, CU counts)
+
+// s_waitcnt vmcnt(0) lgkmcnt(0): every memory operation of this wave, stores included, has completed (gfx9 counts
+// stores in vmcnt; encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+#define FVSR_WAIT_VM0() __builtin_amdgcn_s_waitcnt(7 << 4)
 constexpr int kPoolParts = 4;   // a block mean is summed as 4 runs of 32 tokens, then ((p0 + p1) + (p2 + p3)) / n
 
 // Records the failure message for fvsr_last_error() and returns the status (defined in api.hip).

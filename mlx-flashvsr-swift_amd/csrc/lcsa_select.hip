@@ -262,252 +262,231 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
 // ------------------------------------------------------------------------------------------------------------
 // exact top-k threshold + mask / list emit
 // ------------------------------------------------------------------------------------------------------------
-constexpr int kTopkThreads = 1024;
-constexpr int kTopkRegs = 80;   // elements per thread kept in registers (rows up to 81920 entries)
+// The (k+1)-th largest of each (head, query slice) row of s*Nk probs, k = min(n-1, topk), by an exact select over
+// the fp32 bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0). kThrParts workgroups share a
+// row. Each reads the row's top-12-bit histogram (built by scores_softmax_kernel), finds the bin that holds the
+// threshold and its rank in the bin (all of them find the same), then scans its share of the row and gathers the
+// elements of that bin into the row's candidate area of the workspace. The candidates and the arrival count move
+// as relaxed agent-scope atomics (coherent stores and loads past this XCD's L2), ordered by the wait for the stores
+// and the barrier before the arrival add; the workgroup that arrives last loads the candidates into LDS and
+// resolves the remaining 19 bits by three radix passes (digits [18:11], [10:3], [2:0]). A bin too large for the
+// candidate area (e.g. the threshold falls on the exact zeros outside the local window) makes that last workgroup
+// run a full-row radix select from memory instead: exponent [30:23], then mantissa [22:15], [14:7], [6:0], with the
+// zeros counted by a wave ballot instead of 64 colliding LDS atomics.
+constexpr int kThrParts = 16;           // workgroups per (head, query slice) row
+constexpr int kThrThreads = 256;
+constexpr int kThrLdsCand = 16384;      // candidates the last workgroup holds in LDS
+constexpr int kCandPerBlock = 128;      // candidate words of the workspace per (head, query block)
 
-// One 1024-thread workgroup per (head, query slice) row of s*Nk probs: the (k+1)-th largest, k = min(n-1, topk), by
-// an exact radix select over the fp32 bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0).
-// Digits follow the float layout — exponent [30:23], then mantissa [22:15], [14:7], [6:0] — so the first pass
-// spreads the row over its octaves. The row stays in registers across the passes (re-read from memory only for
-// rows longer than 1024 * kTopkRegs). Exact zeros (key blocks outside the local window) are counted with a wave
-// ballot instead of 64 colliding LDS atomics.
-// One workgroup per (head, query slice) row. First the top-12-bit histogram that scores_softmax_kernel built picks
-// the bin holding the (k+1)-th largest; its elements are gathered into LDS and the remaining 19 bits are resolved
-// there by three small radix passes. A bin holding more than kCand elements (e.g. the threshold falls on the zeros)
-// takes the full-row radix select below instead.
-constexpr int kCand = 16384;
+// per-row control words after the histograms: [0] candidates gathered, [1] workgroups arrived
+__device__ __forceinline__ unsigned* thr_ctl(unsigned* hist12, int rows, int row) {
+  return hist12 + (int64_t)rows * kHistBins + 2 * row;
+}
 
-__global__ __launch_bounds__(kTopkThreads) void topk_threshold_kernel(const float* __restrict__ probs, int nq,
-                                                                      int nk, int q_slices, int topk,
-                                                                      const unsigned* __restrict__ hist12,
-                                                                      float* __restrict__ thr_out) {
-  __shared__ unsigned hist[kTopkThreads / 64][256];
-  __shared__ unsigned tot[256];
-  __shared__ unsigned s_prefix, s_rank;
-  __shared__ unsigned cand[kCand];
-  __shared__ unsigned bins[kHistBins];
-  __shared__ unsigned s_ncand, s_fill;
+// inclusive wave-wide scan (64 lanes)
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned x) {
+  const int lane = threadIdx.x & 63;
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// One radix digit over `count(visit)` of a workgroup of kThrThreads: every (masked) element visited is histogrammed
+// by its digit (u >> shift) & dmask; the digit holding ascending rank `rank` extends `prefix`, `rank` becomes the
+// rank inside it. Zeros matching the prefix are counted by ballot (they all fall in digit 0).
+template <class Visit>
+__device__ __forceinline__ void radix_digit(unsigned (&hist)[kThrThreads / 64][256], unsigned* tot,
+                                            unsigned& prefix, unsigned& rank, unsigned pmask, int shift,
+                                            unsigned dmask, Visit&& visit, unsigned* s_prefix, unsigned* s_rank) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row = blockIdx.x;                       // (head, query slice)
+  for (int e = tid; e < (kThrThreads / 64) * 256; e += kThrThreads) (&hist[0][0])[e] = 0;
+  __syncthreads();
+  unsigned zeros = 0;
+  visit([&](unsigned u) {   // called by every lane of the wave together
+    const bool match = (u & pmask) == prefix;
+    const bool z = match && u == 0u;
+    zeros += __popcll(__ballot(z));
+    wave_hist_add(hist[wave], (u >> shift) & dmask, match && !z);
+  });
+  if (lane == 0 && zeros) atomicAdd(&hist[wave][0], zeros);
+  __syncthreads();
+  {
+    unsigned c = 0;
+#pragma unroll
+    for (int w = 0; w < kThrThreads / 64; ++w) c += hist[w][tid];
+    tot[tid] = c;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const unsigned c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
+    const unsigned lsum = c0 + c1 + c2 + c3;
+    const unsigned incl = wave_incl_scan(lsum);
+    const unsigned excl = incl - lsum;
+    if (rank >= excl && rank < incl) {
+      unsigned cum = excl, d = 4 * lane;
+      const unsigned cs[4] = {c0, c1, c2, c3};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (rank < cum + cs[q]) {
+          d = 4 * lane + q;
+          break;
+        }
+        cum += cs[q];
+      }
+      *s_prefix = prefix | (d << shift);
+      *s_rank = rank - cum;
+    }
+  }
+  __syncthreads();
+  prefix = *s_prefix;
+  rank = *s_rank;
+}
+
+__global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float* __restrict__ probs, int nq,
+                                                                     int nk, int q_slices, int topk,
+                                                                     unsigned* __restrict__ hist12,
+                                                                     unsigned* __restrict__ cand_ws,
+                                                                     float* __restrict__ thr_out) {
+  static_assert(kThrThreads == 256, "the digit scan gives each thread of a 256-thread workgroup one digit");
+  __shared__ unsigned hist[kThrThreads / 64][256];
+  __shared__ unsigned tot[256];
+  __shared__ unsigned wsum[kThrThreads / 64];
+  __shared__ unsigned s_prefix, s_rank, s_ncand, s_arrived;
+  __shared__ unsigned cand[kThrLdsCand];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int part = blockIdx.x, row = blockIdx.y;   // row = (head, query slice)
+  const int rows = gridDim.y;
   const int h = row / q_slices, t = row % q_slices;
   const int sq = nq / q_slices;
-  const int64_t base = ((int64_t)h * nq + (int64_t)t * sq) * nk;
-  const unsigned* bits = (const unsigned*)(probs + base);
+  const unsigned* __restrict__ bits = (const unsigned*)(probs + ((int64_t)h * nq + (int64_t)t * sq) * nk);
   const int64_t n = (int64_t)sq * nk;
   const int64_t k = min<int64_t>(n - 1, topk);
+  const unsigned rank0 = (unsigned)(n - 1 - k);   // ascending rank of the (k+1)-th largest
+  const unsigned cap = (unsigned)min<int64_t>((int64_t)sq * kCandPerBlock, kThrLdsCand);
+  unsigned* const cw = cand_ws + ((int64_t)h * nq + (int64_t)t * sq) * kCandPerBlock;
+  unsigned* const ctl = thr_ctl(hist12, rows, row);
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-  // the whole row, when it fits, with every load in flight at once (thread tid holds elements i*1024 + tid); it
-  // serves both paths below. Padding never matches a bin or a prefix (bit 31 set).
+  // 1. the threshold's bin from the histogram: thread tid owns bins 16 tid .. 16 tid + 15
   const unsigned* hrow = hist12 + (int64_t)row * kHistBins;
-  unsigned hv[kHistBins / kTopkThreads];
+  unsigned hv[16];
 #pragma unroll
-  for (int i = 0; i < kHistBins / kTopkThreads; ++i) hv[i] = hrow[tid * (kHistBins / kTopkThreads) + i];
-  const bool in_regs = n <= (int64_t)kTopkThreads * kTopkRegs;
-  unsigned v[kTopkRegs];
-  if (in_regs) {
-#pragma unroll
-    for (int i = 0; i < kTopkRegs; ++i) {
-      const int64_t e = (int64_t)i * kTopkThreads + tid;
-      v[i] = e < n ? bits[e] : 0xffffffffu;
-    }
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 x = *(const u32x4*)(hrow + 16 * tid + 4 * i);
+    hv[4 * i] = x[0];
+    hv[4 * i + 1] = x[1];
+    hv[4 * i + 2] = x[2];
+    hv[4 * i + 3] = x[3];
   }
+  unsigned psum = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) psum += hv[i];
+  const unsigned incl = wave_incl_scan(psum);
+  if (lane == 63) wsum[wave] = incl;
+  if (tid == 0) s_ncand = 0xffffffffu;
+  __syncthreads();
+  unsigned wbase = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kThrThreads / 64; ++w) {
+    wbase += w < wave ? wsum[w] : 0u;
+    all += wsum[w];
+  }
+  const unsigned zeros = (unsigned)n - all;        // the zeros sort first and sit in bin 0
+  unsigned cum = wbase + incl - psum + (tid > 0 ? zeros : 0u);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int bn = 16 * tid + i;
+    const unsigned c = hv[i] + (bn == 0 ? zeros : 0u);
+    if (rank0 >= cum && rank0 < cum + c) {
+      s_prefix = (unsigned)bn << 19;
+      s_rank = rank0 - cum;
+      s_ncand = c;
+    }
+    cum += c;
+  }
+  __syncthreads();
+  const unsigned bin = s_prefix >> 19, ncand = s_ncand;
+  const bool gather = ncand <= cap;   // workgroup-uniform (every workgroup of the row decides the same)
 
-  // ---- histogram-guided path ----
-  {
-    unsigned part = 0;
-#pragma unroll
-    for (int i = 0; i < kHistBins / kTopkThreads; ++i) {
-      bins[tid * (kHistBins / kTopkThreads) + i] = hv[i];
-      part += hv[i];
-    }
-    // inclusive scan of the per-thread sums (1024 threads)
-    unsigned incl = part;
-    for (int o = 1; o < 64; o <<= 1) {
-      const unsigned y = __shfl_up(incl, o);
-      if (lane >= o) incl += y;
-    }
-    if (lane == 63) tot[wave] = incl;
+  // 2. this workgroup's share of the row: the elements of the bin go to the candidate area. The share is counted
+  // first, so one atomic per workgroup reserves its slots (a returning device-scope atomic per wave and step would
+  // put a memory round trip on every step).
+  if (gather) {
+    const int64_t per = (n + kThrParts - 1) / kThrParts;
+    const int64_t e0 = part * per, e1 = min<int64_t>(n, e0 + per);
+    unsigned mine = 0;
+    for (int64_t e = e0 + tid; e < e1; e += kThrThreads) mine += (bits[e] >> 19) == bin ? 1u : 0u;
+    const unsigned minc = wave_incl_scan(mine);
+    if (lane == 63) wsum[wave] = minc;
     __syncthreads();
-    unsigned wbase = 0;
-    for (int w = 0; w < wave; ++w) wbase += tot[w];
-    unsigned all = 0;
-    for (int w = 0; w < kTopkThreads / 64; ++w) all += tot[w];
-    const unsigned zeros = (unsigned)n - all;          // the zeros sort first and sit in bin 0
-    const unsigned rank = (unsigned)(n - 1 - k);      // ascending rank of the (k+1)-th largest
-    // thread-local exclusive start of its 4 bins, counting the zeros in bin 0
-    unsigned cum = wbase + incl - part + (tid > 0 ? zeros : 0u);
-    if (tid == 0) s_ncand = 0xffffffffu;
-    __syncthreads();
+    unsigned off = minc - mine, wg_total = 0;
 #pragma unroll
-    for (int i = 0; i < kHistBins / kTopkThreads; ++i) {
-      const int bn = tid * (kHistBins / kTopkThreads) + i;
-      const unsigned c = bins[bn] + (bn == 0 ? zeros : 0u);
-      if (rank >= cum && rank < cum + c) {
-        s_prefix = (unsigned)bn << 19;
-        s_rank = rank - cum;
-        s_ncand = c;
-      }
-      cum += c;
+    for (int w = 0; w < kThrThreads / 64; ++w) {
+      off += w < wave ? wsum[w] : 0u;
+      wg_total += wsum[w];
     }
+    if (tid == 0) s_arrived = wg_total ? __hip_atomic_fetch_add(ctl, wg_total, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT) : 0u;
     __syncthreads();
-    const unsigned ncand = s_ncand;
-    if (ncand <= (unsigned)kCand) {   // workgroup-uniform
-      const unsigned bin = s_prefix >> 19;
-      if (in_regs) {
-        // gather the elements of the bin from registers: per-thread counts, a workgroup exclusive scan for the
-        // slots, then the writes (no atomics)
-        unsigned cnt = 0;
-#pragma unroll
-        for (int i = 0; i < kTopkRegs; ++i) cnt += (v[i] >> 19) == bin ? 1u : 0u;
-        unsigned inc = cnt;
-        for (int o = 1; o < 64; o <<= 1) {
-          const unsigned y = __shfl_up(inc, o);
-          if (lane >= o) inc += y;
-        }
-        __syncthreads();   // every thread has read tot[] of the bin search above
-        if (lane == 63) tot[wave] = inc;
-        __syncthreads();
-        unsigned slot = inc - cnt;
-        for (int w = 0; w < wave; ++w) slot += tot[w];
-#pragma unroll
-        for (int i = 0; i < kTopkRegs; ++i)
-          if ((v[i] >> 19) == bin && slot < (unsigned)kCand) cand[slot++] = v[i];
-      } else {
-        // (a counter of its own: s_ncand may still be read by waves that have not reached this point)
-        if (tid == 0) s_fill = 0;
-        __syncthreads();
-        // gather the elements of the bin from memory (wave-aggregated slot reservation)
-        for (int64_t e0 = 0; e0 < n; e0 += kTopkThreads) {
-          const int64_t e = e0 + tid;
-          const unsigned u = e < n ? bits[e] : 0xffffffffu;
-          const bool in = (u >> 19) == bin;
-          const uint64_t m = __ballot(in);
-          unsigned slot = 0;
-          if (lane == 0 && m) slot = atomicAdd(&s_fill, (unsigned)__popcll(m));
-          slot = __shfl(slot, 0);
-          const unsigned at = slot + __popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-          if (in && at < (unsigned)kCand) cand[at] = u;
+    unsigned at = s_arrived + off;
+    if (mine)
+      for (int64_t e = e0 + tid; e < e1; e += kThrThreads) {
+        const unsigned u = bits[e];
+        if ((u >> 19) == bin) {
+          if (at < cap) __hip_atomic_store(cw + at, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ++at;
         }
       }
-      __syncthreads();
-      unsigned prefix = s_prefix, rk = s_rank;
-      unsigned pmask = 0xfff80000u;
-      const int shifts[3] = {11, 3, 0};
-      const unsigned dmasks[3] = {255u, 255u, 7u};
-      for (int pass = 0; pass < 3; ++pass) {
-        const int shift = shifts[pass];
-        const unsigned dmask = dmasks[pass];
-        for (int e = tid; e < (kTopkThreads / 64) * 256; e += kTopkThreads) (&hist[0][0])[e] = 0;
-        __syncthreads();
-        for (int e0 = 0; e0 < (int)ncand; e0 += kTopkThreads) {   // uniform trip count for wave_hist_add
-          const int e = e0 + tid;
-          const unsigned u = e < (int)ncand ? cand[e] : 0xffffffffu;
-          wave_hist_add(hist[wave], (u >> shift) & dmask, (u & pmask) == prefix);
-        }
-        __syncthreads();
-        if (tid < 256) {
-          unsigned c = 0;
-#pragma unroll
-          for (int w = 0; w < kTopkThreads / 64; ++w) c += hist[w][tid];
-          tot[tid] = c;
-        }
-        __syncthreads();
-        if (wave == 0) {
-          const unsigned c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
-          const unsigned lsum = c0 + c1 + c2 + c3;
-          unsigned inc = lsum;
-          for (int o = 1; o < 64; o <<= 1) {
-            const unsigned y = __shfl_up(inc, o);
-            if (lane >= o) inc += y;
-          }
-          const unsigned excl = inc - lsum;
-          if (rk >= excl && rk < inc) {
-            unsigned cm = excl, d = 4 * lane;
-            const unsigned cs[4] = {c0, c1, c2, c3};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              if (rk < cm + cs[q]) { d = 4 * lane + q; break; }
-              cm += cs[q];
-            }
-            s_prefix = prefix | (d << shift);
-            s_rank = rk - cm;
-          }
-        }
-        __syncthreads();
-        prefix = s_prefix;
-        rk = s_rank;
-        pmask |= dmask << shift;
-      }
-      if (tid == 0) thr_out[row] = __uint_as_float(prefix);
-      return;
-    }
-    __syncthreads();
+    __syncthreads();   // every thread has read s_arrived
   }
+  FVSR_WAIT_VM0();   // this wave's candidates are stored at device scope
+  __syncthreads();
+  if (tid == 0) s_arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_arrived != kThrParts - 1) return;   // workgroup-uniform
 
-  // ---- full-row radix select (the bin is too large for LDS) ----
-  unsigned rank = (unsigned)(n - 1 - k);            // ascending rank of the (k+1)-th largest
-  unsigned prefix = 0, pmask = 0x80000000u;
-  if (tid == 0) {
-    s_prefix = 0;
-    s_rank = rank;
-  }
-  const int shifts[4] = {23, 15, 7, 0};
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = shifts[pass];
-    const unsigned dmask = pass == 3 ? 127u : 255u;
-    for (int e = tid; e < (kTopkThreads / 64) * 256; e += kTopkThreads) (&hist[0][0])[e] = 0;
-    __syncthreads();
-    unsigned zeros = 0;   // elements equal to 0 that match the prefix (all fall in digit 0), counted per wave
-    auto count = [&](unsigned u) {
-      const bool match = (u & pmask) == prefix;
-      const bool z = match && u == 0u;
-      zeros += __popcll(__ballot(z));
-      wave_hist_add(hist[wave], (u >> shift) & dmask, match && !z);
-    };
-    if (in_regs) {
-#pragma unroll
-      for (int i = 0; i < kTopkRegs; ++i) count(v[i]);
-    } else {
-      for (int64_t e0 = 0; e0 < n; e0 += kTopkThreads) {
-        const int64_t e = e0 + tid;
-        count(e < n ? bits[e] : 0xffffffffu);
-      }
-    }
-    if (lane == 0 && zeros) atomicAdd(&hist[wave][0], zeros);
-    __syncthreads();
-    if (tid < 256) {
-      unsigned c = 0;
-#pragma unroll
-      for (int w = 0; w < kTopkThreads / 64; ++w) c += hist[w][tid];
-      tot[tid] = c;
-    }
-    __syncthreads();
-    if (wave == 0) {
-      // lane owns bins 4*lane .. 4*lane+3
-      const unsigned c0 = tot[4 * lane], c1 = tot[4 * lane + 1], c2 = tot[4 * lane + 2], c3 = tot[4 * lane + 3];
-      const unsigned lsum = c0 + c1 + c2 + c3;
-      unsigned incl = lsum;
-      for (int o = 1; o < 64; o <<= 1) {
-        const unsigned y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-      }
-      const unsigned excl = incl - lsum;
-      if (rank >= excl && rank < incl) {
-        unsigned cum = excl, d = 4 * lane;
-        const unsigned cs[4] = {c0, c1, c2, c3};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (rank < cum + cs[q]) { d = 4 * lane + q; break; }
-          cum += cs[q];
-        }
-        s_prefix = prefix | (d << shift);
-        s_rank = rank - cum;
-      }
-    }
+  // 3. the last workgroup of the row
+  unsigned prefix, rk;
+  if (gather) {
+    for (unsigned e = tid; e < ncand; e += kThrThreads)
+      cand[e] = __hip_atomic_load(cw + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     prefix = s_prefix;
-    rank = s_rank;
-    pmask |= dmask << shift;
+    rk = s_rank;
+    unsigned pmask = 0xfff80000u;
+    const int shifts[3] = {11, 3, 0};
+    const unsigned dmasks[3] = {255u, 255u, 7u};
+    for (int pass = 0; pass < 3; ++pass) {
+      radix_digit(hist, tot, prefix, rk, pmask, shifts[pass], dmasks[pass], [&](auto&& f) {
+        for (unsigned b0 = 0; b0 < ncand; b0 += kThrThreads) {
+          const unsigned e = b0 + tid;
+          f(e < ncand ? cand[e] : 0xffffffffu);
+        }
+      }, &s_prefix, &s_rank);
+      pmask |= dmasks[pass] << shifts[pass];
+    }
+  } else {
+    if (tid == 0) {
+      s_prefix = 0;
+      s_rank = rank0;
+    }
+    __syncthreads();
+    prefix = 0;
+    rk = rank0;
+    unsigned pmask = 0x80000000u;
+    const int shifts[4] = {23, 15, 7, 0};
+    for (int pass = 0; pass < 4; ++pass) {
+      const unsigned dmask = pass == 3 ? 127u : 255u;
+      radix_digit(hist, tot, prefix, rk, pmask, shifts[pass], dmask, [&](auto&& f) {
+        for (int64_t b0 = 0; b0 < n; b0 += kThrThreads) {
+          const int64_t e = b0 + tid;
+          f(e < n ? bits[e] : 0xffffffffu);
+        }
+      }, &s_prefix, &s_rank);
+      pmask |= dmask << shifts[pass];
+    }
   }
   if (tid == 0) thr_out[row] = __uint_as_float(prefix);
 }
@@ -600,13 +579,20 @@ int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int hea
   return FVSR_OK;
 }
 
-size_t hist12_bytes(int heads, int q_slices) { return (size_t)heads * q_slices * kHistBins * sizeof(unsigned); }
+// the (head, query slice) histograms and, after them, two control words per row (all cleared before a selection)
+size_t hist12_bytes(int heads, int q_slices) {
+  return (size_t)heads * q_slices * (kHistBins + 2) * sizeof(unsigned);
+}
 
-int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, const unsigned* hist,
-                     float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream) {
+// candidate area of the threshold select for `heads` x `nq` query blocks
+size_t topk_cand_bytes(int heads, int64_t nq) { return (size_t)heads * nq * kCandPerBlock * sizeof(unsigned); }
+
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, unsigned* hist,
+                     unsigned* cand, float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt,
+                     hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;
-  hipLaunchKernelGGL(topk_threshold_kernel, dim3(heads * q_slices), dim3(kTopkThreads), 0, stream, probs, nq, nk,
-                     q_slices, topk, hist, thr);
+  hipLaunchKernelGGL(topk_threshold_kernel, dim3(kThrParts, heads * q_slices), dim3(kThrThreads), 0, stream, probs,
+                     nq, nk, q_slices, topk, hist, cand, thr);
   FVSR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(topk_emit_kernel, dim3((heads * nq + 3) / 4), dim3(256), 0, stream, probs, thr, heads, nq, nk,
                      q_slices, mask_out, sel, kidx, kcnt);

@@ -5,7 +5,8 @@ import ctypes as C
 import os
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG, "lib", "libfvsr_lcsa.so")
+# FVSR_LCSA_LIB selects another build of the same library (e.g. one compiled with different launch parameters)
+LIB_PATH = os.environ.get("FVSR_LCSA_LIB") or os.path.join(_PKG, "lib", "libfvsr_lcsa.so")
 
 OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_OUT_OF_MEMORY, ERR_CAPACITY, ERR_STATE = range(7)
 DTYPE_F32, DTYPE_BF16 = 0, 1
