@@ -5,7 +5,9 @@
  * reference function is cited beside each declaration. Conventions:
  *   - plain pointers and sizes only; device pointers are HIP device memory owned by the caller;
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream); no entry point synchronises the
- *     host except where stated;
+ *     host, except that a call which needs more context workspace than the context holds grows it (hipFree +
+ *     hipMalloc, and hipFree synchronises the device): fvsr_ctx_reserve / fvsr_ctx_reserve_block size it up front,
+ *     after which calls of at most that size allocate nothing;
  *   - every function returns an fvsr_status; on failure fvsr_last_error() returns a message for the calling thread;
  *   - token buffers are token-major (L, H*128) in window order (128-token windows ordered (nf, nh, nw), tokens in a
  *     window ordered (wf, wh, ww)), exactly the reference's (1, L, H*128) layout (DiT.swift:111-118,514);
@@ -196,10 +198,18 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const void
                         float* mask_out, float* probs_out, void* stream);
 
 /* ---- (f3) the dense parts of the DiT block ------------------------------------------------------------------ */
+/* No reference counterpart (MLX allocates lazily): make the DiT-block entry points allocation-free for blocks of up to
+ * `tokens` tokens (heads * 128 channels, FFN width ffn_dim, ctx_len context tokens) over a ring window of up to
+ * `key_tokens` keys. Creates the context's hipBLASLt handle and 64 MB GEMM workspace, grows the block workspace
+ * (about (8 C + F) * tokens * 2 bytes) and the select/attention workspace. */
+int fvsr_ctx_reserve_block(fvsr_ctx* ctx, int heads, int64_t tokens, int ffn_dim, int ctx_len, int64_t key_tokens);
+size_t fvsr_ctx_block_workspace_bytes(const fvsr_ctx* ctx);
+
 /* `Linear` (MLX, DiT.swift:319-321,371): y = x W^T + b on hipBLASLt, bf16 in/out, fp32 accumulate. x: (rows,
  * in_features); weight: (out_features, in_features) row-major; bias: (out_features) or NULL; gelu != 0 applies the
  * tanh-form GELU of `GELU(approximation: .tanh)` (DiT.swift:371) to the fp32 result before the bf16 store. Feature
- * counts must be multiples of 8. The first call on a context creates its hipBLASLt handle and 64 MB GEMM workspace. */
+ * counts must be multiples of 8. The first call on a context creates its hipBLASLt handle and 64 MB GEMM workspace
+ * (fvsr_ctx_reserve_block creates it up front). */
 int fvsr_linear(fvsr_ctx* ctx, const void* x, int64_t rows, int in_features, const void* weight, int out_features,
                 const void* bias, int gelu, void* y, void* stream);
 
@@ -230,7 +240,8 @@ int fvsr_dit_cross_kv(fvsr_ctx* ctx, const fvsr_dit_block_weights* w, int heads,
  * norm3 (eps), modulation, the q/k/v projections, fvsr_lcsa_layer_qkv on `ring` (selection + attention + cache
  * append/evict; topk, mode, local window and RoPE as there), the o projection and gated residual, the
  * cross-attention over w->cross_k / cross_v, and the FFN with its gated residual. Activations live in a block
- * workspace of the context (about (8 * C + F) * L * 2 bytes), grown on the first call of a size. */
+ * workspace of the context (about (8 * C + F) * L * 2 bytes), grown on the first call of a size unless
+ * fvsr_ctx_reserve_block sized it. */
 int fvsr_dit_block(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const fvsr_dit_block_weights* w, const void* t_mod,
                    void* x, int n_new_slices, int t0, float eps, const float* rope_tables, const uint8_t* local_dev,
                    int topk, int mode, void* stream);

@@ -439,8 +439,8 @@ static int check_epilogue(int dtype, const void* q, const void* k, const void* v
                "window (2, 8, 8) must tile (f, h, w)");
   int rc = check_heads(heads);
   if (rc) return rc;
-  FVSR_REQUIRE(heads * 128 * esize(dtype) / 16 <= 1024, FVSR_ERR_UNSUPPORTED,
-               "the epilogue handles at most 1024 16-byte vectors per token");
+  FVSR_REQUIRE(heads * 128 * esize(dtype) / 16 <= 384, FVSR_ERR_UNSUPPORTED,
+               "the epilogue handles at most 384 16-byte vectors per token (64 lanes x 6)");
   FVSR_REQUIRE(t0 >= 0 && t0 + f <= 1024 && h <= 1024 && w <= 1024, FVSR_ERR_INVALID_ARG,
                "token positions must lie inside the 1024-row RoPE tables");
   FVSR_REQUIRE(eps >= 0.f, FVSR_ERR_INVALID_ARG, "eps must be >= 0");
@@ -517,6 +517,18 @@ int fvsr_kv_ring_reset(fvsr_kv_ring* r) {
   std::fill(r->head.begin(), r->head.end(), 0);
   std::fill(r->count.begin(), r->count.end(), 0);
   return FVSR_OK;
+}
+
+// a layer's ring position before a layer call, so that a call failing after its append leaves the ring as it
+// found it (the slots the append wrote are free again) instead of holding one slice more than the trim rule allows
+struct RingMark {
+  int head, count;
+};
+static RingMark ring_mark(const fvsr_kv_ring* r, int layer) { return RingMark{r->head[layer], r->count[layer]}; }
+static int ring_rewind(fvsr_kv_ring* r, int layer, RingMark m, int rc) {
+  r->head[layer] = m.head;
+  r->count[layer] = m.count;
+  return rc;
 }
 
 static int check_layer(const fvsr_kv_ring* r, int layer) {
@@ -708,6 +720,7 @@ int fvsr_lcsa_layer(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* qW, i
   const int64_t nq = ceil_div(lq, kBlock);
   const Carve cv = carve(r->heads, nq, nk_after, r->C);
   if ((rc = ensure_ws(ctx, cv.total))) return rc;
+  const RingMark mark = ring_mark(r, layer);
   if ((rc = fvsr_kv_ring_append(r, layer, k_new, v_new, n_new_slices, layout, stream))) return rc;
   const int nk = r->count[layer] * r->s;
   char* ws = (char*)ctx->ws;
@@ -717,11 +730,11 @@ int fvsr_lcsa_layer(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* qW, i
   rc = select_impl(ctx, r->dtype, qW, lq, r->layer_pooled(layer), true, nullptr, (int64_t)nk * kBlock,
                    r->map(layer), nk, r->heads, q_slices, r->s, local_dev, topk, mask_out, probs_out, kidx, kcnt,
                    sel, st);
-  if (rc) return rc;
+  if (rc) return ring_rewind(r, layer, mark, rc);
   int use = mode;
   if (use == FVSR_ATTN_AUTO) fvsr_attention_mode_auto(topk, r->s, nk, kAutoThreshold, nullptr, &use);
   rc = attention_ring_impl(ctx, r, layer, qW, lq, kidx, kcnt, nk, sel, use == FVSR_ATTN_DENSE, o, st);
-  if (rc) return rc;
+  if (rc) return ring_rewind(r, layer, mark, rc);
   return fvsr_kv_ring_evict(r, layer);
 }
 
@@ -748,6 +761,7 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q
   const Carve cv = carve(r->heads, nq, nk_after, r->C);
   if ((rc = ensure_ws(ctx, cv.total))) return rc;
   char* ws = (char*)ctx->ws;
+  const RingMark mark = ring_mark(r, layer);
   // the pooled queries and the histogram reset ride in the append's pooling launches
   if ((rc = append_qkv_impl(r, layer, q, k, v, n_new_slices, t0, norm_q_weight, norm_k_weight, eps, rope_tables,
                             q_work, st, (float*)(ws + cv.partial), (float*)(ws + cv.pq), (unsigned*)(ws + cv.hist),
@@ -760,11 +774,11 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q
   rc = select_impl(ctx, r->dtype, q_work, lq, r->layer_pooled(layer), true, nullptr, (int64_t)nk * kBlock,
                    r->map(layer), nk, r->heads, q_slices, r->s, local_dev, topk, mask_out, probs_out, kidx, kcnt,
                    sel, st, true);
-  if (rc) return rc;
+  if (rc) return ring_rewind(r, layer, mark, rc);
   int use = mode;
   if (use == FVSR_ATTN_AUTO) fvsr_attention_mode_auto(topk, r->s, nk, kAutoThreshold, nullptr, &use);
   rc = attention_ring_impl(ctx, r, layer, q_work, lq, kidx, kcnt, nk, sel, use == FVSR_ATTN_DENSE, o, st, true);
-  if (rc) return rc;
+  if (rc) return ring_rewind(r, layer, mark, rc);
   return fvsr_kv_ring_evict(r, layer);
 }
 
@@ -831,6 +845,25 @@ static int check_block_weights(const fvsr_dit_block_weights* w, bool need_self, 
 }
 
 extern "C" {
+
+int fvsr_ctx_reserve_block(fvsr_ctx* ctx, int heads, int64_t tokens, int ffn_dim, int ctx_len, int64_t key_tokens) {
+  FVSR_REQUIRE(ctx != nullptr, FVSR_ERR_INVALID_ARG, "ctx is NULL");
+  int rc = check_heads(heads);
+  if (rc) return rc;
+  FVSR_REQUIRE(tokens > 0 && ffn_dim > 0 && ctx_len > 0 && key_tokens > 0, FVSR_ERR_INVALID_ARG,
+               "tokens, ffn_dim, ctx_len and key_tokens must be > 0");
+  const int C = heads * kHeadDim;
+  const int64_t nq = ceil_div(tokens, kBlock);
+  FVSR_HIP_CHECK(hipSetDevice(ctx->device));
+  if ((rc = ensure_blas(ctx))) return rc;
+  const BlockCarve bc = block_carve(tokens, C, ffn_dim, (int64_t)heads * nq, (int)ceil_div(ctx_len, kBlock));
+  if ((rc = ensure_block_ws(ctx, bc.total))) return rc;
+  // the layer call's selection and attention over the ring window, and the cross-attention over the context
+  const int64_t lk = std::max<int64_t>(key_tokens, ctx_len);
+  return ensure_ws(ctx, carve(heads, nq, ceil_div(lk, kBlock), C).total);
+}
+
+size_t fvsr_ctx_block_workspace_bytes(const fvsr_ctx* ctx) { return ctx ? ctx->block_ws_bytes : 0; }
 
 int fvsr_linear(fvsr_ctx* ctx, const void* x, int64_t rows, int in_features, const void* weight, int out_features,
                 const void* bias, int gelu, void* y, void* stream) {

@@ -47,6 +47,16 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   return xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
 }
 
+// inclusive scan over the 64 lanes of a wave
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned x) {
+  const int lane = threadIdx.x & 63;
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
 // Logical key block j of the key range -> first token row of that block in the K/V buffer.
 // Plain buffers: plain_key_map() (slot_head 0, capacity 1, slice_blocks 65536 >= Nk) gives row j*128.
 // Ring: block j lives in slot (head + j / s) % capacity at block j % s of that slot.

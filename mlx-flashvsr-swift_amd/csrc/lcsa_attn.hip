@@ -127,10 +127,15 @@ __device__ __forceinline__ int swz_v(int r) { return (r & 3) << 2; }
 // is loaded with s_mov_b32 from an address computed outside the asm. GFX9 requires one wait state between an SALU
 // write of M0 and an LDS DMA that reads it; the compiler inserts it for its own code but not inside an asm
 // statement, so the s_nop is written out.
+// The row's offset `voff` and the block's offset `boff` are added into the one VGPR offset (the SGPR offset is 0):
+// the raw buffer's range check covers the VGPR offset and the instruction offset, not the SGPR offset, so only an
+// offset held there makes a row past the buffer (a ragged last block, a listed index outside [0, nk), the tiles past
+// the end of the walk, whose block offset is the buffer's size) load zeros without touching memory.
 template <int OFF>
-__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_base, int voff, int soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds_base + OFF),
-               "v"(voff), "s"(rsrc), "s"(soff));
+__device__ __forceinline__ void dma16(u32x4 rsrc, uint32_t lds_base, int voff, int boff) {
+  const uint32_t off = (uint32_t)voff + (uint32_t)boff;   // < 2^31 + 2^17: no wrap
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_base + OFF),
+               "v"(off), "s"(rsrc));
 }
 
 __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
@@ -588,90 +593,80 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 }
 
 // Rows (head, query block) for the persistent bf16 walk, and its work counter. One workgroup. First a counting sort
-// by decreasing key-list length in bins of 8 blocks (the dense walk: every non-empty row is a full walk). The first
-// `grid` rows of that order are each workgroup's first row (workgroup b takes item b without the counter): they are
-// re-sorted by row id (head-major, neighbouring query blocks together) and dealt so that the workgroups of one XCD
-// (b % 8, dispatch is round-robin over the XCDs) start on one contiguous range of rows, whose key lists overlap, so
-// the XCD's L2 serves the key blocks they share. The counter then hands out the rest, longest first, from item
-// `grid` on. The order does not affect results.
+// by decreasing key-list length in bins of 8 blocks (255 bins; longer lists share the last one; the dense walk: every
+// non-empty row is a full walk). The first `grid` rows of that order are each workgroup's first row (workgroup b
+// takes item b without the counter): they are re-sorted by row id (head-major, neighbouring query blocks together)
+// and dealt so that the workgroups of one XCD (b % 8, dispatch is round-robin over the XCDs) start on one contiguous
+// range of rows, whose key lists overlap, so the XCD's L2 serves the key blocks they share. The counter then hands
+// out the rest, longest first, from item `grid` on. The order does not affect results. Scans are wave-wide (shuffles)
+// with one step across the waves, so the kernel needs a handful of barriers.
 __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
                                                           int dense, int grid, int32_t* __restrict__ order,
                                                           int32_t* __restrict__ counter) {
-  constexpr int kBins = 4096;
+  constexpr int kBins = 256;
+  constexpr int kWords = 4096;   // row-id bitmap words: the bitmap rank serves up to 32 x 4096 rows
   __shared__ int bin_start[kBins];
-  __shared__ int part[1024];
-  const int tid = threadIdx.x;
-  for (int b = tid; b < kBins; b += 1024) bin_start[b] = 0;
+  __shared__ int wtot[16];
+  __shared__ __attribute__((aligned(16))) int first[kMaxPersistentWgs];   // padded with INT_MAX (ranks nothing)
+  __shared__ unsigned bm[kWords];
+  __shared__ int wpre[kWords];                                            // set bits in the words before word w
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < kBins) bin_start[tid] = 0;
   __syncthreads();
   auto bin_of = [&](int r) -> int {   // bin 0 = the longest lists
     const int c = kcnt[r];
-    const int len = c <= 0 ? 0 : (dense ? 1 : min(((min(c, nk_stride) + 7) >> 3), kBins - 1));
+    const int len = c <= 0 ? 0 : (dense ? 1 : min((min(c, nk_stride) + 7) >> 3, kBins - 1));
     return kBins - 1 - len;
   };
   for (int r = tid; r < rows; r += 1024) atomicAdd(&bin_start[bin_of(r)], 1);
   __syncthreads();
-  // exclusive scan of the 4096 bin counts: 4 bins per thread, then a scan of the 1024 thread sums
-  int v[4], sum = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[i] = bin_start[4 * tid + i];
-    sum += v[i];
-  }
-  part[tid] = sum;
-  __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {
-    const int x = tid >= d ? part[tid - d] : 0;
+  // exclusive scan of the 256 bin counts by waves 0..3
+  {
+    const int v = tid < kBins ? bin_start[tid] : 0;
+    const int incl = (int)wave_incl_scan((unsigned)v);
+    if (tid < kBins && lane == 63) wtot[wave] = incl;
     __syncthreads();
-    part[tid] += x;
-    __syncthreads();
-  }
-  int run = part[tid] - sum;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bin_start[4 * tid + i] = run;
-    run += v[i];
+    if (tid < kBins) {
+      int base = 0;
+      for (int w = 0; w < wave; ++w) base += wtot[w];
+      bin_start[tid] = base + incl - v;
+    }
   }
   __syncthreads();
   // the first n_first items (one per workgroup) stay in LDS: re-sorted by row id, they are dealt so that XCD x
   // (workgroups b with b % 8 == x) holds one contiguous range of them
   const int n_first = min(min(grid, rows), kMaxPersistentWgs);
-  __shared__ __attribute__((aligned(16))) int first[kMaxPersistentWgs];   // padded with INT_MAX (ranks nothing)
   for (int i = n_first + tid; i < kMaxPersistentWgs; i += 1024) first[i] = 0x7fffffff;
+  const bool use_bitmap = rows <= kWords * 32;
+  const int words = use_bitmap ? (rows + 31) / 32 : 0;
+  for (int w = tid; w < words; w += 1024) bm[w] = 0u;
   for (int r = tid; r < rows; r += 1024) {
     const int pos = atomicAdd(&bin_start[bin_of(r)], 1);
     if (pos < n_first) first[pos] = r;
     else order[pos] = r;
   }
   __syncthreads();
-  // rank of each first row among them by row id: a bitmap over the row ids (the bin counts are free now) and a scan
-  // of its per-word popcounts; beyond 32 x 4096 rows, a scan of the first rows themselves
-  const bool use_bitmap = rows <= kBins * 32;
-  __shared__ int wpre[kBins];   // set bits in the words before word w
-  unsigned* const bm = (unsigned*)bin_start;
+  // rank of each first row among them by row id: a bitmap over the row ids and a scan of its per-word popcounts;
+  // beyond 32 x 4096 rows, a scan of the first rows themselves
   if (use_bitmap) {
-    for (int w = tid; w < kBins; w += 1024) bm[w] = 0u;
-    __syncthreads();
     for (int i = tid; i < n_first; i += 1024) atomicOr(&bm[first[i] >> 5], 1u << (first[i] & 31));
     __syncthreads();
     int c[4], csum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      c[i] = __popc(bm[4 * tid + i]);
+      const int w = 4 * tid + i;
+      c[i] = w < words ? __popc(bm[w]) : 0;
       csum += c[i];
     }
-    part[tid] = csum;
+    const int incl = (int)wave_incl_scan((unsigned)csum);
+    if (lane == 63) wtot[wave] = incl;
     __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-      const int x = tid >= d ? part[tid - d] : 0;
-      __syncthreads();
-      part[tid] += x;
-      __syncthreads();
-    }
-    int crun = part[tid] - csum;
+    int run = incl - csum;
+    for (int w = 0; w < wave; ++w) run += wtot[w];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      wpre[4 * tid + i] = crun;
-      crun += c[i];
+      if (4 * tid + i < words) wpre[4 * tid + i] = run;
+      run += c[i];
     }
     __syncthreads();
   }

@@ -283,16 +283,6 @@ __device__ __forceinline__ unsigned* thr_ctl(unsigned* hist12, int rows, int row
   return hist12 + (int64_t)rows * kHistBins + 2 * row;
 }
 
-// inclusive wave-wide scan (64 lanes)
-__device__ __forceinline__ unsigned wave_incl_scan(unsigned x) {
-  const int lane = threadIdx.x & 63;
-  for (int o = 1; o < 64; o <<= 1) {
-    const unsigned y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
 // One radix digit over `count(visit)` of a workgroup of kThrThreads: every (masked) element visited is histogrammed
 // by its digit (u >> shift) & dmask; the digit holding ascending rank `rank` extends `prefix`, `rank` becomes the
 // rank inside it. Zeros matching the prefix are counted by ballot (they all fall in digit 0).

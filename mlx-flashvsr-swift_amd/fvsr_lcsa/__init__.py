@@ -139,6 +139,14 @@ class Context:
     def workspace_bytes(self) -> int:
         return int(lib.fvsr_ctx_workspace_bytes(self.handle))
 
+    def reserve_block(self, heads: int, tokens: int, ffn_dim: int, ctx_len: int, key_tokens: int):
+        """Size everything a DiT block call of up to `tokens` tokens over a ring window of up to `key_tokens` keys
+        needs (hipBLASLt state, block and select/attention workspaces), so later block calls allocate nothing."""
+        call("fvsr_ctx_reserve_block", self.handle, heads, tokens, ffn_dim, ctx_len, key_tokens)
+
+    def block_workspace_bytes(self) -> int:
+        return int(lib.fvsr_ctx_block_workspace_bytes(self.handle))
+
     def local_device(self, local, s: int) -> torch.Tensor:
         """Device copy of an (s, s) local window mask, memoised by content (the reference memoises per geometry,
         DiT.swift:464-470). The library reads s * s bytes from it."""

@@ -51,6 +51,8 @@ SIGNATURES = {
     "fvsr_kv_ring_append_qkv": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _vp]),
     "fvsr_lcsa_layer_qkv": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, C.c_float, _vp, _vp, _i, _i, _vp,
                                  _vp, _vp, _vp, _vp]),
+    "fvsr_ctx_reserve_block": (_i, [_vp, _i, _i64, _i, _i, _i64]),
+    "fvsr_ctx_block_workspace_bytes": (_sz, [_vp]),
     "fvsr_linear": (_i, [_vp, _vp, _i64, _i, _vp, _i, _vp, _i, _vp, _vp]),
     "fvsr_dit_cross_kv": (_i, [_vp, _vp, _i, _vp, _i, C.c_float, _vp, _vp, _vp]),
     "fvsr_dit_block": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, C.c_float, _vp, _vp, _i, _i, _vp]),

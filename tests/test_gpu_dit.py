@@ -136,3 +136,31 @@ def test_dit_block_matches_oracle(dev, heads, ffn, bh, bw, rng, ctx_len, chunks)
         print(f"  rel err {err:.3e}", flush=True)
         assert err < 5e-3
     ring.close()
+
+
+def test_reserved_block_calls_allocate_nothing(dev):
+    """fvsr_ctx_reserve_block sizes the hipBLASLt state, the block workspace and the select/attention workspace up
+    front: block calls of at most the reserved size then leave both workspaces as they are (no hipFree / hipMalloc
+    inside the call)."""
+    heads, ffn, bh, bw, ctx_len = 2, 512, 3, 3, 100
+    r = np.random.default_rng(5)
+    c, s = heads * 128, bh * bw
+    W = _weights(r, c, ffn, heads)
+    blk = fvsr_lcsa.DiTBlock({k: _bf(v, dev) for k, v in W.items()}, heads)
+    blk.set_context(_bf(L.to_bf16(r.standard_normal((ctx_len, c)).astype(np.float32)), dev))
+    ring = fvsr_lcsa.KVRing(1, heads, bh, bw, capacity=4, kv_len=3, device=dev.index or 0)
+    fresh = fvsr_lcsa.Context(dev.index or 0)      # a context no earlier call has grown
+    ring.ctx = fresh
+    tokens, key_tokens = 2 * s * 128, 4 * s * 128   # the largest chunk (2 slices) over the fullest window (4 slices)
+    fresh.reserve_block(heads, tokens, ffn, ctx_len, key_tokens)
+    ws, bws = fresh.workspace_bytes(), fresh.block_workspace_bytes()
+    assert ws > 0 and bws > 0
+    tm = _bf(L.to_bf16((r.standard_normal((6, c)) * 0.1).astype(np.float32)), dev)
+    local = L.local_block_mask(bh, bw, 3)
+    for n_new, t0 in [(2, 0), (1, 4), (1, 6)]:
+        x = _bf(L.to_bf16(r.standard_normal((2 * n_new * 64 * s, c)).astype(np.float32)), dev)
+        blk.forward(ring, 0, x, tm, n_new, t0, local, 40)
+        torch.cuda.synchronize()
+        assert torch.isfinite(x.float()).all()
+        assert (fresh.workspace_bytes(), fresh.block_workspace_bytes()) == (ws, bws)
+    ring.close()

@@ -97,6 +97,23 @@ def test_epilogue_rejects_bad_geometry(dev):
         fvsr_lcsa.qkv_epilogue(q, q, q, 2, 8, 8, 12, 1023, wq, wq)     # positions past the 1024-row tables
 
 
+def test_epilogue_width_limit_is_checked_before_launch(dev):
+    """A token of at most 384 16-byte vectors (64 lanes x 6 registers) runs; a wider one is refused by validation
+    with FVSR_ERR_UNSUPPORTED. fp32: 12 heads = 384 vectors run, 13 heads = 416 vectors are refused."""
+    for heads, ok in ((12, True), (13, False)):
+        c = heads * 128
+        q = torch.randn((2 * 8 * 8, c), device=dev)
+        w = torch.ones(c, device=dev)
+        if ok:
+            qo, _, _ = fvsr_lcsa.qkv_epilogue(q, q, q, 2, 8, 8, heads, 0, w, w)
+            torch.cuda.synchronize()
+            assert torch.isfinite(qo).all()
+        else:
+            with pytest.raises(fvsr_lcsa.FVSRError, match="384") as ei:
+                fvsr_lcsa.qkv_epilogue(q, q, q, 2, 8, 8, heads, 0, w, w)
+            assert ei.value.status == 2
+
+
 def test_ring_append_qkv_wrapping_append(dev):
     """An append whose slices wrap past the ring's last slot (capacity 4, kv_len 2: slices 3 and 0) is pooled in two
     pieces; the held window and its pooled keys still equal the plain epilogue's."""

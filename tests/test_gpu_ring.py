@@ -132,25 +132,3 @@ def test_ring_errors(dev):
     assert ei.value.status == 5                      # capacity
     with pytest.raises(fvsr_lcsa.FVSRError):
         fvsr_lcsa.KVRing(1, 1, 1, 2, capacity=3, kv_len=3)
-
-
-def test_streaming_schedule_shapes_1920x1152(dev):
-    """The real 1920x1152 geometry (s = 135): chunk 0 attends 405 x 405 blocks, later chunks 135 x 540
-    (PORTING-SPEC.md:129), through layer calls with the reference's default top-k 16199 and local range 11."""
-    heads, bh, bw = 12, 9, 15
-    s = bh * bw
-    local = O.local_block_mask(bh, bw, 11)
-    topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
-    ring = fvsr_lcsa.KVRing(1, heads, bh, bw, 4, 3, torch.bfloat16)
-    gen = torch.Generator(device=dev).manual_seed(0)
-    for n in (3, 1, 1):
-        L = n * s * 128
-        q = torch.randn((L, heads * 128), device=dev, generator=gen).to(torch.bfloat16)
-        kn = torch.randn((L, heads * 128), device=dev, generator=gen).to(torch.bfloat16)
-        vn = torch.randn((L, heads * 128), device=dev, generator=gen).to(torch.bfloat16)
-        o, m, _ = ring.layer_call(0, q, kn, vn, n, n, local, topk, want_mask=True)
-        assert m.shape == (heads, n * s, (3 if n == 3 else 4) * s)
-        per_row = m.reshape(heads * n, -1).sum(1)
-        assert (per_row <= topk).all()
-        assert torch.isfinite(o.float()).all()
-        assert ring.slices(0) == 3
