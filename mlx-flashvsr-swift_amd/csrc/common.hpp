@@ -121,7 +121,8 @@ struct AttnArgs {
   int64_t kv_rows;       // token rows physically present in the k/v buffers (buffer-load range)
   float c;               // softmax scale * log2(e)
   int32_t* order;        // (H * nq) rows, longest key list first (bf16 persistent walk; workspace)
-  int32_t* counter;      // next index into `order` (workspace; zeroed by the order kernel)
+  int32_t* counter;      // per-XCD queue counters of the walk, counter[8 x] for XCD x (workspace, 256 bytes; set by
+                         // the order kernel)
   int o_nbh, o_nbw;      // > 0: write o in natural (f, h, w) token order of an (8 o_nbh, 8 o_nbw) grid (the
                          // reference's windowReverse, DiT.swift:121-126) instead of window order
   // output row of window-order query row r

@@ -150,6 +150,24 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 
 }  // namespace
 
+// The next position of the per-XCD queues of attn_order_kernel's dealt order, starting with this workgroup's XCD
+// (dispatch is round-robin over the XCDs: XCD of workgroup b = b % 8), then stealing from the others; `rows` when
+// every queue is empty. Queue y holds, wave by wave, the positions w * grid + y + 8 i, i < per_y = ceil((grid - y)
+// / 8); its counter (counters[8 y]) starts past the first wave, which the workgroups take without it. Positions
+// grow with the counter, so the first one past `rows` means the queue is empty. Called by one thread.
+__device__ __forceinline__ int next_dealt_item(int32_t* counters, int rows) {
+  const int grid = (int)gridDim.x;
+  for (int t = 0; t < kXcds; ++t) {
+    const int y = ((int)blockIdx.x + t) & (kXcds - 1);
+    const int per = (grid - y + kXcds - 1) / kXcds;
+    if (per <= 0) continue;
+    const int k = atomicAdd(counters + 8 * y, 1);
+    const int p = (k / per) * grid + y + kXcds * (k % per);
+    if (p < rows) return p;
+  }
+  return rows;
+}
+
 // LDS operand requests of chunk / pair j >= 2 (j = 0, 1: micro-round 0), in micro-rounds of a step with QG query
 // groups per wave: 7 (QG 2) or 4 (QG 1) micro-rounds before the QK MFMA that uses them
 template <int QG>
@@ -170,9 +188,12 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int rows = a.heads * a.nq;
-  // Persistent: the grid is sized to the resident workgroups. Workgroup b starts on item b (attn_order_kernel puts
-  // the longest rows there, dealt by XCD), then takes the next item from the counter, longest key list first, so
-  // the long rows start early and the short ones fill in behind them.
+  // Persistent: the grid is sized to the resident workgroups. attn_order_kernel sorts the rows longest key list
+  // first and deals every wave of gridDim.x of them by XCD (re-sorted by row id, XCD x holds positions x, x + 8, ..
+  // of the wave: one contiguous row range, whose key lists overlap). Workgroup b starts on position b of the first
+  // wave; after that it takes the next position of its XCD's queue (positions x, x + 8, .. of the first wave, then
+  // of the second, ...) and, once that queue is empty, of the other XCDs' queues in turn. So the long rows start
+  // early, the rows running together on one XCD share key blocks in its L2, and the short ones balance the tail.
   bool first_item = true;
   for (;;) {
   int item;
@@ -180,7 +201,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     item = blockIdx.x;
     first_item = false;
   } else {
-    if (tid == 0) item_s = atomicAdd(counter, 1);
+    if (tid == 0) item_s = next_dealt_item(counter, rows);
     __syncthreads();
     item = item_s;
     __syncthreads();
@@ -592,22 +613,22 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   }   // next row
 }
 
-// Rows (head, query block) for the persistent bf16 walk, and its work counter. One workgroup. First a counting sort
-// by decreasing key-list length in bins of 8 blocks (255 bins; longer lists share the last one; the dense walk: every
-// non-empty row is a full walk). The first `grid` rows of that order are each workgroup's first row (workgroup b
-// takes item b without the counter): they are re-sorted by row id (head-major, neighbouring query blocks together)
-// and dealt so that the workgroups of one XCD (b % 8, dispatch is round-robin over the XCDs) start on one contiguous
-// range of rows, whose key lists overlap, so the XCD's L2 serves the key blocks they share. The counter then hands
-// out the rest, longest first, from item `grid` on. The order does not affect results. Scans are wave-wide (shuffles)
-// with one step across the waves, so the kernel needs a handful of barriers.
+// Rows (head, query block) for the persistent bf16 walk, and the per-XCD queue counters. One workgroup. First a
+// counting sort by decreasing key-list length in bins of 8 blocks (255 bins; longer lists share the last one; the
+// dense walk: every non-empty row is a full walk). Then every wave of `grid` consecutive items of that order (one
+// item per workgroup) is re-sorted by row id (head-major, neighbouring query blocks together) and dealt so that XCD x
+// (workgroups b with b % 8 == x, dispatch is round-robin over the XCDs) holds positions x, x + 8, .. of the wave:
+// one contiguous range of rows, whose key lists overlap, so the XCD's L2 serves the key blocks they share.
+// next_dealt_item hands the positions out per XCD. The order does not affect results. Scans are wave-wide
+// (shuffles) with one step across the waves.
 __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
                                                           int dense, int grid, int32_t* __restrict__ order,
-                                                          int32_t* __restrict__ counter) {
+                                                          int32_t* __restrict__ counters) {
   constexpr int kBins = 256;
   constexpr int kWords = 4096;   // row-id bitmap words: the bitmap rank serves up to 32 x 4096 rows
   __shared__ int bin_start[kBins];
   __shared__ int wtot[16];
-  __shared__ __attribute__((aligned(16))) int first[kMaxPersistentWgs];   // padded with INT_MAX (ranks nothing)
+  __shared__ __attribute__((aligned(16))) int first[kMaxPersistentWgs];   // one wave; padded with INT_MAX
   __shared__ unsigned bm[kWords];
   __shared__ int wpre[kWords];                                            // set bits in the words before word w
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -633,65 +654,66 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
     }
   }
   __syncthreads();
-  // the first n_first items (one per workgroup) stay in LDS: re-sorted by row id, they are dealt so that XCD x
-  // (workgroups b with b % 8 == x) holds one contiguous range of them
-  const int n_first = min(min(grid, rows), kMaxPersistentWgs);
-  for (int i = n_first + tid; i < kMaxPersistentWgs; i += 1024) first[i] = 0x7fffffff;
+  for (int r = tid; r < rows; r += 1024) order[atomicAdd(&bin_start[bin_of(r)], 1)] = r;
+  __threadfence_block();
+  __syncthreads();
+  grid = min(grid, kMaxPersistentWgs);
   const bool use_bitmap = rows <= kWords * 32;
   const int words = use_bitmap ? (rows + 31) / 32 : 0;
-  for (int w = tid; w < words; w += 1024) bm[w] = 0u;
-  for (int r = tid; r < rows; r += 1024) {
-    const int pos = atomicAdd(&bin_start[bin_of(r)], 1);
-    if (pos < n_first) first[pos] = r;
-    else order[pos] = r;
-  }
-  __syncthreads();
-  // rank of each first row among them by row id: a bitmap over the row ids and a scan of its per-word popcounts;
-  // beyond 32 x 4096 rows, a scan of the first rows themselves
-  if (use_bitmap) {
-    for (int i = tid; i < n_first; i += 1024) atomicOr(&bm[first[i] >> 5], 1u << (first[i] & 31));
+  for (int w0 = 0; w0 < rows; w0 += grid) {
+    const int nw = min(grid, rows - w0);
+    for (int i = tid; i < kMaxPersistentWgs; i += 1024) first[i] = i < nw ? order[w0 + i] : 0x7fffffff;
+    for (int w = tid; w < words; w += 1024) bm[w] = 0u;
     __syncthreads();
-    int c[4], csum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int w = 4 * tid + i;
-      c[i] = w < words ? __popc(bm[w]) : 0;
-      csum += c[i];
-    }
-    const int incl = (int)wave_incl_scan((unsigned)csum);
-    if (lane == 63) wtot[wave] = incl;
-    __syncthreads();
-    int run = incl - csum;
-    for (int w = 0; w < wave; ++w) run += wtot[w];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (4 * tid + i < words) wpre[4 * tid + i] = run;
-      run += c[i];
-    }
-    __syncthreads();
-  }
-  const int n4 = (n_first + 31) / 32 * 8;   // int4 groups to scan, a multiple of the unroll
-  for (int i = tid; i < n_first; i += 1024) {
-    const int r = first[i];
-    int rank = 0;   // rows are distinct: ranks are a permutation of 0 .. n_first - 1
+    // rank of each row of the wave among them by row id: a bitmap over the row ids and a scan of its per-word
+    // popcounts; beyond 32 x 4096 rows, a scan of the wave's rows themselves
     if (use_bitmap) {
-      rank = wpre[r >> 5] + __popc(bm[r >> 5] & ((1u << (r & 31)) - 1u));
-    } else {
-#pragma unroll 8
-      for (int j = 0; j < n4; ++j) {
-        const int4 f = reinterpret_cast<const int4*>(first)[j];
-        rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+      for (int i = tid; i < nw; i += 1024) atomicOr(&bm[first[i] >> 5], 1u << (first[i] & 31));
+      __syncthreads();
+      int c[4], csum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = 4 * tid + i;
+        c[i] = w < words ? __popc(bm[w]) : 0;
+        csum += c[i];
       }
+      const int incl = (int)wave_incl_scan((unsigned)csum);
+      if (lane == 63) wtot[wave] = incl;
+      __syncthreads();
+      int run = incl - csum;
+      for (int w = 0; w < wave; ++w) run += wtot[w];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (4 * tid + i < words) wpre[4 * tid + i] = run;
+        run += c[i];
+      }
+      __syncthreads();
     }
-    // XCD x holds m_x = (n_first - x + 7) / 8 workgroups, b = x, x + 8, ..; ranks s_x .. s_x + m_x - 1 go to it
-    int x = 0, s0 = 0;
-    while (s0 + (n_first - x + kXcds - 1) / kXcds <= rank) {
-      s0 += (n_first - x + kXcds - 1) / kXcds;
-      ++x;
+    const int n4 = (nw + 31) / 32 * 8;   // int4 groups to scan, a multiple of the unroll
+    for (int i = tid; i < nw; i += 1024) {
+      const int r = first[i];
+      int rank = 0;   // rows are distinct: ranks are a permutation of 0 .. nw - 1
+      if (use_bitmap) {
+        rank = wpre[r >> 5] + __popc(bm[r >> 5] & ((1u << (r & 31)) - 1u));
+      } else {
+#pragma unroll 8
+        for (int j = 0; j < n4; ++j) {
+          const int4 f = reinterpret_cast<const int4*>(first)[j];
+          rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+        }
+      }
+      // XCD x holds m_x = (nw - x + 7) / 8 positions x, x + 8, ..; ranks s_x .. s_x + m_x - 1 go to it
+      int x = 0, s0 = 0;
+      while (s0 + (nw - x + kXcds - 1) / kXcds <= rank) {
+        s0 += (nw - x + kXcds - 1) / kXcds;
+        ++x;
+      }
+      order[w0 + (rank - s0) * kXcds + x] = r;
     }
-    order[(rank - s0) * kXcds + x] = r;
+    __syncthreads();
   }
-  if (tid == 0) *counter = n_first;
+  // queue y's counter starts past the first wave (the workgroups take it without the counters)
+  if (tid < kXcds) counters[8 * tid] = (grid - tid + kXcds - 1) / kXcds;
 }
 
 // ------------------------------------------------------------------------------------------------------------
