@@ -47,6 +47,7 @@ def parse_args():
                          "6-latent-frame first chunk and 4 chunks of 2 latent frames; append + select + attention + "
                          "evict per layer call; prints its own JSON line")
     ap.add_argument("--layers", type=int, default=30)
+    ap.add_argument("--iid", action="store_true", help="with --stream: i.i.d. N(0,1) Q/K instead of a smooth field")
     ap.add_argument("--from-projections", action="store_true",
                     help="with --stream: feed each layer the q/k/v projections in natural token order "
                          "(normQ/normK + RoPE + window partition + ring append fused, output window-reversed)")
@@ -176,8 +177,11 @@ def stream_bench(args):
     """The attention stack of the streaming DiT at 1920x1152 (the reference's geometry: s = 135 blocks per slice, a
     first chunk of 6 latent frames = 3 slices, then chunks of 2 latent frames = 1 slice; KV window 3 slices;
     default top-k 16199, local range 11; Pipeline.swift:22-23,68,95-102; DiT.swift:478-538). Each layer call runs
-    append + select + block-sparse attention + evict through fvsr_lcsa_layer. Q/K/V of each chunk are synthetic
-    (N(0,1), per-head RMS norm, 3-D RoPE at the chunk's latent frames), resident in HBM and shared by the layers."""
+    append + select + block-sparse attention + evict through fvsr_lcsa_layer. Q/K/V of each chunk are synthetic,
+    resident in HBM and shared by the layers: by default Q/K are a smooth field over the 14 latent frames plus noise
+    (with --from-projections: WanRMSNorm weights of about 2, so the pooled scores of a row span a wide range, as
+    for real features); --iid draws them N(0,1). Without --from-projections Q/K are per-head RMS-normed with 3-D
+    RoPE at the chunk's latent frames."""
     import torch
 
     import fvsr_lcsa
@@ -193,12 +197,25 @@ def stream_bench(args):
     gen = torch.Generator(device=dev).manual_seed(args.seed or 0)
     data = []
     proj = args.from_projections
-    wq = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
-    wk = (0.5 + torch.rand(C, generator=gen, device=dev)).to(torch.bfloat16)
+    smooth = not args.iid
+    if smooth:
+        cgen = torch.Generator().manual_seed(args.seed or 0)
+        field = synth.smooth_field(14, lat_h, lat_w, C, cgen)
+        wscale = 2.0
+    else:
+        wscale = 1.0
+    wq = (wscale * (0.5 + torch.rand(C, generator=gen, device=dev))).to(torch.bfloat16)
+    wk = (wscale * (0.5 + torch.rand(C, generator=gen, device=dev))).to(torch.bfloat16)
     for n, t0 in chunks:
         f = 2 * n
         L = f * lat_h * lat_w
-        q, k, v = (torch.randn((L, C), generator=gen, device=dev) for _ in range(3))
+        if smooth:
+            sl = slice(t0 * lat_h * lat_w, (t0 + f) * lat_h * lat_w)
+            q = (field[sl] + 0.5 * torch.randn((L, C), generator=cgen)).to(dev)
+            k = (field[sl] + 0.5 * torch.randn((L, C), generator=cgen)).to(dev)
+            v = torch.randn((L, C), generator=gen, device=dev)
+        else:
+            q, k, v = (torch.randn((L, C), generator=gen, device=dev) for _ in range(3))
         if proj:   # the projections themselves, natural token order; the layer call normalises and rotates
             data.append(tuple(x.to(torch.bfloat16).contiguous() for x in (q, k, v)))
             continue
@@ -257,8 +274,10 @@ def stream_bench(args):
         "higher_is_better": False,
         "n_gpus": 1,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1), per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)",
-        "config": {"workload": "stream_1920x1152_bf16" + ("_from_projections" if proj else ""), "layers": args.layers, "heads": H, "head_dim": 128,
+        "data": ("synthetic, seeded: " + ("Q/K a smooth field + N(0, 0.25) noise" if smooth else "Q/K N(0,1)") +
+                 ("; WanRMSNorm weights " + ("~2" if smooth else "~1") if proj else "; per-head RMS norm") +
+                 " + 3-D RoPE; no checkpoint"),
+        "config": {"workload": "stream_1920x1152_bf16" + ("_from_projections" if proj else "") + ("_iid" if not smooth else ""), "layers": args.layers, "heads": H, "head_dim": 128,
                    "spatial_blocks_per_slice": s, "local_range": 11, "topk": topk, "kv_window_slices": 3,
                    "chunks": [{"query_blocks": n * s, "key_blocks": min(n + (3 if c else 0), 4) * s}
                               for c, (n, _) in enumerate(chunks)]},

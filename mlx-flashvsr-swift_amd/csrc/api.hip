@@ -60,7 +60,7 @@ int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* 
 int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int w, int C, bool to_windows,
                          hipStream_t stream);
 
-constexpr int kMaxSelectKeyBlocks = 1920;    // scores stage LDS: (8 x (128 + Nk) + 64 x 132) fp32 + 8 x Nk B
+constexpr int kMaxSelectKeyBlocks = 1920;    // scores stage LDS: (8 x (128 + Nk) + 2 x 64 x 132) fp32 + 8 x Nk B
 constexpr double kAutoThreshold = 0.45;      // DiT.swift:210
 
 static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }

@@ -33,17 +33,15 @@ typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 typedef __attribute__((address_space(3))) char lds_char;
 
 
-// O^T += A B on the matrix core with the accumulator in AGPRs. The library is compiled with the MFMA VGPR form
-// (-amdgpu-mfma-vgpr-form) so the score MFMAs, whose results the VALU reads, write VGPRs: an AGPR result would cost
-// one v_accvgpr_read per score, and those (like v_dot2) stall behind a running MFMA. Only this accumulation keeps the
-// AGPR form, written out here. Hazards the compiler does not see through the asm: the B operand (P) is written by
-// the VALU a barrier before it is read; A (V^T) comes from ds_read, whose lgkmcnt wait the compiler inserts;
-// successive accumulations into one block are >= 7 MFMAs apart; acc_drain() runs before the VALU touches the
-// accumulators again.
+// O^T += A B on the matrix core. The library is compiled with the MFMA VGPR form (-amdgpu-mfma-vgpr-form): the score
+// MFMAs, whose results the VALU reads, and this accumulation write VGPRs (the working set, about 230 registers, fits
+// the 256 of two waves per SIMD). The accumulation is the compiler's builtin, so it sees every hazard and keeps one
+// register assignment for O across the walk's control paths (the reference raise); successive accumulations into
+// one block are >= 7 MFMAs apart.
 __device__ __forceinline__ void mfma_acc(f32x16& acc, const bf16x8& a, const bf16x8& b) {
-  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
 }
-// >= 19 wait states: an 8-pass MFMA result may be read or overwritten by the VALU afterwards
+// >= 19 wait states after the last MFMA of a walk (the compiler also inserts what it needs)
 __device__ __forceinline__ void acc_drain() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory"); }
 
 // Lazy online-softmax rescale. The running reference max m_run (log2 domain, per query row) is raised only when a
@@ -89,12 +87,15 @@ __device__ __forceinline__ void static_for(F&& f) {
 // While tile T is processed (step T), K of tile T+4 and V of tile T+2 are requested; they are waited for two steps
 // later, before the step that reads them.
 //
-// Softmax with a fixed reference per query row: Q is prescaled by log2(e)/sqrt(128) and one extra rank-2 MFMA step
-// per tile adds -m (the row's reference, the exact max of its first tile) and -2^100 for keys of the tile that do
-// not take part (ragged end, unselected block of the dense walk), so P = exp2(S^T) straight from the accumulators.
-// The largest partial row sum is tracked; a row whose scores outgrow the reference by 2^32, or underflow, makes the
-// workgroup redo its rows exactly (row-max pass, then attention with that max). The result is the softmax whatever
-// the reference is.
+// Softmax with a lazily raised reference per query row: S = K Q^T in fp32 from the bf16 inputs (one extra rank-1
+// MFMA per tile adds -2^100 for keys that do not take part: ragged end, unselected block of the dense walk), then
+// P = exp2(c S - m) with one v_fma per score (c = log2(e)/sqrt(128), applied to the fp32 scores as the reference
+// does, SparseAttention.swift:96; m, the row's reference, first the exact max of its first tile). A tile whose
+// partial row sum exceeds 2^32 (its scores outgrew the reference by about 27 or more, in log2 units) raises the
+// reference to the tile's max: its exponentials are recomputed and O and l rescaled (a wave-uniform branch, rare:
+// rows with sharp attention raise it a few times). Rows whose exponentials all underflowed (a reference from a tile
+// with no valid key, and every real score 2^-32 below it) make the workgroup redo its rows exactly (row-max pass,
+// then attention with that max). The result is the softmax whatever the reference is.
 //
 // Software pipeline per wave, step T: the exponentials of S(T) are issued between the MFMAs of PV(T-1) and QK(T+1),
 // so the VALU work hides under matrix-core time. The walk is unrolled by one 128-key block (4 steps); block indices
@@ -107,6 +108,7 @@ constexpr int kTileBytes = kTileKeys * kRowBytes;      // 8 KB
 constexpr int kSlots = 4;                              // per ring: slot of tile T = T mod 4 = its quarter of the block
 constexpr int kVRing = kSlots * kTileBytes;            // byte offset of the V ring
 constexpr float kMaskedScore = -1.2676506e30f;         // -2^100: exp2 of a masked key is exactly 0
+constexpr float kGrowSum = 4294967296.f;               // 2^32: a larger partial row sum raises the reference
 constexpr int kMaxPersistentWgs = 1024;                // persistent grid cap (the order kernel's first-row deal)
 
 // 16-byte chunk swizzles. K: the 8 (or 16) lanes one ds_read_b128 cycle serves read 8 (16) consecutive rows of one
@@ -223,8 +225,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   const uint8_t* __restrict__ srow = DENSE ? sel + (int64_t)row_id * a.nk : nullptr;
   const int nblocks = DENSE ? a.nk : min(cnt, a.nk_stride);
 
-  // Q as the B operand of S^T = K Q^T, prescaled by c: group q holds queries qb*128 + kQW*wave + 32*q + l32,
-  // lane (query, k-half g) dims 16t + 8g .. +7
+  // Q as the B operand of S^T = K Q^T (the bf16 inputs as they are; the scale c is applied to the fp32 scores):
+  // group q holds queries qb*128 + kQW*wave + 32*q + l32, lane (query, k-half g) dims 16t + 8g .. +7
   bf16x8 qop[QG][8];
 #pragma unroll
   for (int q = 0; q < QG; ++q) {
@@ -233,10 +235,6 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     for (int t = 0; t < 8; ++t) {
       bf16x8 x = bf16x8{};
       if (qrow < a.lq) x = *(const bf16x8*)(Q + qrow * a.ld + hc + 16 * t + 8 * g);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = (bf16)((float)x[e] * a.c);
-      // Q is only ever an MFMA operand: keep it in AGPRs, leaving the VGPRs to S, P and the LDS operands
-      asm volatile("" : "+a"(x));
       qop[q][t] = x;
     }
   }
@@ -314,31 +312,35 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     v_off[dt] = vr * kRowBytes + (((4 * dt + 2 * (G & 1) + ((mm & 3) >> 1)) ^ swz_v(vr)) << 4) + (mm & 1) * 8;
 
   f32x16 acc[QG][4];
-  float l_run[QG], m_row[QG], part_max[QG];
-  // the extra MFMA step, a v_mfma_f32_32x32x8_bf16 (k = 8, half the cost of a k = 16 step): A lane (key l32, g = 0)
-  // holds k-slots {1, masked}, B lane (query, g = 0) {-m, -2^100}, all other k-slots 0
-  i16x4 bext[QG];
+  float l_run[QG], m_row[QG], part_max[QG], m_ref[QG], negm[QG];
+  constexpr float kNoKey = -1e29f;   // a raw row max below this saw masked keys only
+  const float c_scale = a.c;         // softmax scale * log2(e)
+  // the reference (log2 units, fp32) of each query row: P = exp2(c S - m), one v_fma per score
   auto set_ref = [&](int q, float m) {
-    bf16x4 b = bf16x4{};
-    if (g == 0) {
-      b[0] = (bf16)(-m);
-      b[1] = (bf16)kMaskedScore;
-    }
-    bext[q] = __builtin_bit_cast(i16x4, b);
+    m_ref[q] = m;
+    negm[q] = -m;
   };
+  // the reference of a raw row max (masked keys only: 0)
+  auto ref_of = [&](float mx) -> float { return mx > kNoKey ? mx * c_scale : 0.f; };
+  // the extra MFMA step, a v_mfma_f32_32x32x8_bf16 (k = 8, half the cost of a k = 16 step): A lane (key l32, g = 0)
+  // holds k-slot {masked}, B lane (query, g = 0) {-2^100}, all other k-slots 0: keys that do not take part score
+  // -2^100 and their exponentials are exactly 0
+  i16x4 bext;
+  {
+    bf16x4 b = bf16x4{};
+    if (g == 0) b[0] = (bf16)kMaskedScore;
+    bext = __builtin_bit_cast(i16x4, b);
+  }
   auto aext = [&](int valid) -> i16x4 {
     bf16x4 x = bf16x4{};
-    if (g == 0) {
-      x[0] = (bf16)1.0f;
-      x[1] = l32 >= valid ? (bf16)1.0f : (bf16)0.0f;
-    }
+    if (g == 0) x[0] = l32 >= valid ? (bf16)1.0f : (bf16)0.0f;
     return __builtin_bit_cast(i16x4, x);
   };
   auto mfma_ext = [&](const i16x4& ax, const i16x4& bx) -> f32x16 {
     return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ax, bx, f32x16{}, 0, 0, 0);
   };
   lds_char* const lds = (lds_char*)(uintptr_t)smem_lds;
-  // S^T = K Q^T - m (keys that do not take part: - 2^100) for both groups, K from ring slot SLOT
+  // S^T = K Q^T (keys that do not take part: - 2^100) for both groups, K from ring slot SLOT
   auto qk = [&](auto slot_c, int valid, f32x16 (&s)[QG]) {
     constexpr int SLOT = decltype(slot_c)::value;
     bf16x8 kk[8];
@@ -346,7 +348,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     for (int t = 0; t < 8; ++t) kk[t] = *(const lds_bf16x8*)(lds + SLOT * kTileBytes + k_off[t]);
     const i16x4 ax = aext(valid);
 #pragma unroll
-    for (int q = 0; q < QG; ++q) s[q] = mfma_ext(ax, bext[q]);
+    for (int q = 0; q < QG; ++q) s[q] = mfma_ext(ax, bext);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -384,7 +386,6 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     else FVSR_WAIT_VM_LGKM0(0);
     __builtin_amdgcn_s_barrier();
   };
-  constexpr float kNoKey = -1e29f;   // a row max below this saw masked keys only
   using C0 = std::integral_constant<int, 0>;
   using C1 = std::integral_constant<int, 1>;
   using C2 = std::integral_constant<int, 2>;
@@ -423,10 +424,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
                                              : 0,
          sA);
 #pragma unroll
-      for (int q = 0; q < QG; ++q) {
-        const float mx = row_max(sA[q]);
-        set_ref(q, (float)(bf16)(mx > kNoKey ? mx : 0.f));
-      }
+      for (int q = 0; q < QG; ++q) set_ref(q, ref_of(row_max(sA[q])));
       __builtin_amdgcn_s_barrier();   // every wave is done with K slot 0 before the walk refills it
     }
     // prologue = virtual steps -4 .. -1: K(0..3) and V(-2..1); V(-2), V(-1) are zeros, so step 0's PV of the
@@ -438,14 +436,9 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     sync_steps(3);   // K(0) landed
     qk(C0{}, sub_valid(n0, 0), sA);
     if (MODE == 0 && !DENSE) {
-      // reference = the exact row max of tile 0; the tile is then recomputed with it inside the accumulator, the
-      // same arithmetic as every later tile (and as the dense walk)
+      // reference = the exact row max of tile 0 (scaled), as the dense walk's pre-step computes it
 #pragma unroll
-      for (int q = 0; q < QG; ++q) {
-        const float mx = row_max(sA[q]);
-        set_ref(q, (float)(bf16)(mx > kNoKey ? mx : 0.f));
-      }
-      qk(C0{}, sub_valid(n0, 0), sA);
+      for (int q = 0; q < QG; ++q) set_ref(q, ref_of(row_max(sA[q])));
     }
 #pragma unroll
     for (int q = 0; q < QG; ++q)
@@ -506,7 +499,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
             if constexpr (attn_read_at<QG>(J) == I) read_ops(J);
           });
           if constexpr (I < QG) {
-            s_nxt[I] = mfma_ext(ax, bext[I]);
+            s_nxt[I] = mfma_ext(ax, bext);
           } else {
             constexpr int c = (I - QG) / (2 * QG), w = (I - QG) % (2 * QG);
             if constexpr (w < QG) {
@@ -522,7 +515,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           if constexpr (I < 16 * QG) {
             // S(T) entry idx of group q; fp32 sums (v_dot2 would wait for the matrix core)
             constexpr int q = I >> 4, idx = I & 15;
-            const float x = __builtin_amdgcn_exp2f(s_cur[q][idx]);
+            const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[q][idx], c_scale, negm[q]));
             if constexpr ((I & 1) == 0) {
               x_even = x;
             } else {
@@ -535,11 +528,45 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           __builtin_amdgcn_sched_barrier(0);
         };
         static_for<0, 17 * QG>(micro);
+        float part[QG];
+        bool grow = false;
 #pragma unroll
         for (int q = 0; q < QG; ++q) {
-          const float part = sum[q][0] + sum[q][1];
-          l_run[q] += part;
-          if (MODE == 0) part_max[q] = fmaxf(part_max[q], part);
+          part[q] = sum[q][0] + sum[q][1];
+          grow |= !(pair_max(part[q]) <= kGrowSum);   // also inf / NaN
+        }
+        if (__ballot(grow) != 0) {
+          // raise the reference of the rows that grew to their max in S(T); the other rows keep theirs (their
+          // scale is 1 and every operation below is exact and changes nothing)
+          acc_drain();
+#pragma unroll
+          for (int q = 0; q < QG; ++q) {
+            const bool gq = !(pair_max(part[q]) <= kGrowSum);
+            const float m_new = gq ? row_max(s_cur[q]) * c_scale : m_ref[q];
+            const float sc = __builtin_amdgcn_exp2f(m_ref[q] - m_new);
+            set_ref(q, m_new);
+            float t[2] = {0.f, 0.f};
+#pragma unroll
+            for (int idx = 1; idx < 16; idx += 2) {
+              const float x0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[q][idx - 1], c_scale, negm[q]));
+              const float x1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[q][idx], c_scale, negm[q]));
+              p_cur[q][idx >> 3][(idx & 7) - 1] = (bf16)x0;
+              p_cur[q][idx >> 3][idx & 7] = (bf16)x1;
+              t[(idx >> 1) & 1] += x0 + x1;
+            }
+            part[q] = t[0] + t[1];
+            l_run[q] *= sc;
+            part_max[q] *= sc;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) acc[q][dt][i] *= sc;
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+          l_run[q] += part[q];
+          part_max[q] = fmaxf(part_max[q], part[q]);
         }
       }
       // keep every instruction of this step on its side of the barrier
@@ -568,15 +595,13 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   };
 
   run(std::integral_constant<int, 0>{});
-  // rows whose scores outgrew the first-tile reference by 2^32, or whose exponentials all underflowed: redo the
-  // workgroup exactly (row max pass, then attention with that max); workgroup-uniform so the barriers match
+  // rows whose exponentials all underflowed (the reference came from a tile with no valid key and every score is
+  // far below it): redo the workgroup exactly (row max pass, then attention with that max); workgroup-uniform so the
+  // barriers match
   {
     bool bad = false;
 #pragma unroll
-    for (int q = 0; q < QG; ++q) {
-      const float pm = pair_max(part_max[q]);
-      bad |= !(pm <= 4294967296.f) || pm < 2.3283064e-10f;
-    }
+    for (int q = 0; q < QG; ++q) bad |= !(pair_max(part_max[q]) >= 2.3283064e-10f);
     int* flag = (int*)smem;
     if (tid == 0) flag[0] = 0;
     __syncthreads();
@@ -587,7 +612,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     if (redo) {
       run(std::integral_constant<int, 1>{});
 #pragma unroll
-      for (int q = 0; q < QG; ++q) m_row[q] = (float)(bf16)(m_row[q] > kNoKey ? m_row[q] : 0.f);
+      for (int q = 0; q < QG; ++q) m_row[q] = ref_of(m_row[q]);
       run(std::integral_constant<int, 2>{});
     }
   }

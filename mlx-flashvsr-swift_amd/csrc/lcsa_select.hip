@@ -12,10 +12,10 @@
 //   pool_part_kernel     one workgroup per run of 32 tokens of a block: coalesced 16-byte loads, fp32 sums (Q
 //                        and K, or Q and the new ring keys, in one launch); the means come from pool_finish_kernel
 //                        (kv_ring.hip) in a fixed order, which also clears the histogram below
-//   scores_softmax_kernel one workgroup per (8 query blocks, head): pooled-key rows staged through LDS in coalesced
-//                         chunks of 64 keys and read once per 8 query rows, scores + local mask in LDS, one wave per
-//                         row for max / exp / sum / normalise; it also counts the nonzero probs of each (head,
-//                         query slice) per top-12-bit bin
+//   scores_softmax_kernel one 8-wave workgroup per (8 query blocks, head): pooled-key rows staged through LDS in
+//                         coalesced chunks of 64 keys, two chunks side by side, read once per 8 query rows; scores
+//                         + local mask in LDS, one wave per row for max / exp / sum / normalise; it also counts the
+//                         nonzero probs of each (head, query slice) per top-12-bit bin
 //   topk_threshold_kernel one 1024-thread workgroup per (head, query slice): exact (k+1)-th largest over the fp32
 //                         bit patterns (probs are >= 0, so bit order = value order): the row is loaded into
 //                         registers at once, the histogram picks the bin, its elements are gathered to LDS and
@@ -106,8 +106,9 @@ __device__ __forceinline__ void wave_hist_add(unsigned* h, unsigned key, bool va
 // ------------------------------------------------------------------------------------------------------------
 // scores + softmax
 // ------------------------------------------------------------------------------------------------------------
-constexpr int kScoreRows = 8;   // query blocks per workgroup (2 per wave of 256 threads)
-constexpr int kKeyChunk = 64;   // key blocks staged in LDS at a time
+constexpr int kScoreRows = 8;   // query blocks per workgroup (one per wave in the softmax)
+constexpr int kScoreThreads = 512;   // 8 waves: two halves of 4 stage alternate key chunks side by side
+constexpr int kKeyChunk = 64;   // key blocks staged in LDS at a time by one half
 constexpr int kKStride = kHeadDim + 4;   // padded LDS row of a pooled key (floats)
 constexpr int kHistBins = 4096; // top-12-bit bins (bits 30..19) of the prob bit patterns
 
@@ -115,19 +116,19 @@ constexpr int kHistBins = 4096; // top-12-bit bins (bits 30..19) of the prob bit
 // local: (s, s) bytes; probs: (H, nq, nk).
 // hist: (H * q_slices, kHistBins) u32, the count of the nonzero probs of each (head, query slice) row per top-12-bit
 // bin (bits 30..19; zeros are left out); zeroed before the launch.
-__global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __restrict__ pq,
-                                                             const float* __restrict__ pk, KeyMap kmap, int C,
-                                                             int nq, int nk, int s,
-                                                             const uint8_t* __restrict__ local,
-                                                             float* __restrict__ probs,
-                                                             unsigned* __restrict__ hist, int q_slices) {
+__global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const float* __restrict__ pq,
+                                                                       const float* __restrict__ pk, KeyMap kmap,
+                                                                       int C, int nq, int nk, int s,
+                                                                       const uint8_t* __restrict__ local,
+                                                                       float* __restrict__ probs,
+                                                                       unsigned* __restrict__ hist, int q_slices) {
   extern __shared__ float sm[];
   float* qs = sm;                                      // [kScoreRows][128]
-  float* ks = qs + kScoreRows * kHeadDim;              // [kKeyChunk][kKStride]
+  float* ks = qs + kScoreRows * kHeadDim;              // [2 halves][kKeyChunk][kKStride]
   // the workgroup histograms of the (up to) two query slices of its rows, [2][kHistBins]: they reuse the key chunk
-  // staging once the scores are done (keeping the LDS of a workgroup small enough for 3 per CU)
+  // staging once the scores are done
   unsigned* lhist = (unsigned*)ks;
-  float* ss = ks + kKeyChunk * kKStride;               // [kScoreRows][nk]
+  float* ss = ks + 2 * kKeyChunk * kKStride;           // [kScoreRows][nk]
   const int sw = min(s, nk);                           // local-window columns that key blocks 0..nk-1 use
   uint8_t* lm = (uint8_t*)(ss + kScoreRows * nk);      // [kScoreRows][sw] local-window bytes of this group's rows
   const int h = blockIdx.y;
@@ -135,31 +136,35 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
   const int tid = threadIdx.x;
   const int sq = nq / q_slices;                 // query blocks per slice
   const int t_first = i0 / sq;
-  for (int e = tid; e < kScoreRows * kHeadDim; e += blockDim.x) {
+  for (int e = tid; e < kScoreRows * kHeadDim; e += kScoreThreads) {
     const int r = e / kHeadDim, d = e % kHeadDim;
     qs[e] = (i0 + r < nq) ? pq[(int64_t)(i0 + r) * C + h * kHeadDim + d] : 0.f;
   }
-  for (int e = tid; e < kScoreRows * sw; e += blockDim.x) {
+  for (int e = tid; e < kScoreRows * sw; e += kScoreThreads) {
     const int r = e / sw, c = e - r * sw;
     lm[e] = local[((i0 + r) % s) * s + c];
   }
   __syncthreads();
   const float sqrt_d = sqrtf((float)kHeadDim);
-  // Key blocks in chunks of 64: the chunk's pooled-key rows (64 x 512 B) are read with coalesced 16-byte loads
-  // (each wave load covers two whole rows) into padded LDS rows, the loads of the next two chunks in flight while
-  // the current one is multiplied. The products run on the matrix cores in fp32 (v_mfma_f32_16x16x4_f32): wave w takes keys
-  // 16w .. 16w + 15 of the chunk against the 8 query rows (padded to 16). Lane l holds A = Q[l % 16][32 (l / 16) + t]
-  // and B = K[16w + l % 16][32 (l / 16) + t] at step t (the reduction index of step t, lane group g is dim 32 g + t,
-  // so each lane reads 32 contiguous floats), and the 16 x 16 product lands as D[4 (l / 16) + v][l % 16], v < 4.
+  // Key blocks in chunks of 64, the two halves of the workgroup on alternate chunks (half 0: chunks 0, 2, ..; half
+  // 1: chunks 1, 3, ..) with a staging buffer each: the chunk's pooled-key rows (64 x 512 B) are read with coalesced
+  // 16-byte loads (each wave load covers two whole rows) into padded LDS rows, the loads of the half's next chunk in
+  // flight while the current one is multiplied. The products run on the matrix cores in fp32
+  // (v_mfma_f32_16x16x4_f32): wave w of a half takes keys 16w .. 16w + 15 of the chunk against the 8 query rows
+  // (padded to 16). Lane l holds A = Q[l % 16][32 (l / 16) + t] and B = K[16w + l % 16][32 (l / 16) + t] at step t
+  // (the reduction index of step t, lane group g is dim 32 g + t, so each lane reads 32 contiguous floats), and the
+  // 16 x 16 product lands as D[4 (l / 16) + v][l % 16], v < 4.
   const int wave = tid >> 6, lane = tid & 63;
+  const int half = wave >> 2, hw = wave & 3, htid = tid & 255;
   const int li = lane & 15, lg = lane >> 4;
   const float* kbase = pk + h * kHeadDim;
-  constexpr int kLoads = kKeyChunk * (kHeadDim / 4) / 256;   // 16-byte loads per thread per chunk
+  float* kst = ks + half * kKeyChunk * kKStride;
+  constexpr int kLoads = kKeyChunk * (kHeadDim / 4) / 256;   // 16-byte loads per thread of a half per chunk
   auto load_chunk = [&](f32x4 (&pre)[kLoads], int j0) {
     const int nj = min(kKeyChunk, nk - j0);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int e = i * 256 + tid, jj = e >> 5, c4 = e & 31;
+      const int e = i * 256 + htid, jj = e >> 5, c4 = e & 31;
       if (jj < nj) pre[i] = *(const f32x4*)(kbase + (kmap.row(j0 + jj) / kBlock) * C + 4 * c4);
     }
   };
@@ -172,19 +177,19 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
     qa[t + 2] = x[2];
     qa[t + 3] = x[3];
   }
-  // one chunk: its rows to LDS, the loads of the chunk after next into the same registers, the products
+  // one round: each half stages its chunk (j0 < nk) and multiplies it; both halves take part in the barriers
   auto chunk = [&](f32x4 (&pre)[kLoads], int j0) {
-    const int nj = min(kKeyChunk, nk - j0);
-    __syncthreads();   // the previous chunk's rows have been read
+    const int nj = j0 < nk ? min(kKeyChunk, nk - j0) : 0;
+    __syncthreads();   // the previous round's rows have been read
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int e = i * 256 + tid, jj = e >> 5, c4 = e & 31;
-      if (jj < nj) *(f32x4*)(ks + jj * kKStride + 4 * c4) = pre[i];
+      const int e = i * 256 + htid, jj = e >> 5, c4 = e & 31;
+      if (jj < nj) *(f32x4*)(kst + jj * kKStride + 4 * c4) = pre[i];
     }
     __syncthreads();
     if (j0 + 2 * kKeyChunk < nk) load_chunk(pre, j0 + 2 * kKeyChunk);
-    if (16 * wave < nj) {   // wave-uniform; rows of keys past nj hold stale data and are not stored
-      const float* krow = ks + (16 * wave + li) * kKStride + 32 * lg;
+    if (16 * hw < nj) {   // wave-uniform; rows of keys past nj hold stale data and are not stored
+      const float* krow = kst + (16 * hw + li) * kKStride + 32 * lg;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int t = 0; t < 32; t += 4) {
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 2], kb[2], acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 3], kb[3], acc, 0, 0, 0);
       }
-      const int jj = 16 * wave + li, j = j0 + jj;
+      const int jj = 16 * hw + li, j = j0 + jj;
       if (4 * lg < kScoreRows && jj < nj) {   // rows 4 lg .. 4 lg + 3 that are query rows of the group
         const int ksp = j % s;
 #pragma unroll
@@ -205,18 +210,13 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
       }
     }
   };
-  f32x4 pa[kLoads], pb[kLoads];
-  load_chunk(pa, 0);
-  if (kKeyChunk < nk) load_chunk(pb, kKeyChunk);
-  for (int j0 = 0; j0 < nk; j0 += 2 * kKeyChunk) {
-    chunk(pa, j0);
-    if (j0 + kKeyChunk < nk) chunk(pb, j0 + kKeyChunk);
-  }
+  f32x4 pre[kLoads];
+  load_chunk(pre, half * kKeyChunk);
+  for (int j0 = 0; j0 < nk; j0 += 2 * kKeyChunk) chunk(pre, j0 + half * kKeyChunk);
   __syncthreads();
-  for (int e = tid; e < 2 * kHistBins; e += blockDim.x) lhist[e] = 0u;
+  for (int e = tid; e < 2 * kHistBins; e += kScoreThreads) lhist[e] = 0u;
   __syncthreads();
-  const int nwaves = blockDim.x >> 6;
-  for (int r = wave; r < kScoreRows; r += nwaves) {
+  for (int r = wave; r < kScoreRows; r += kScoreThreads / 64) {
     if (i0 + r >= nq) break;
     float* srow = ss + r * nk;
     float mx = -INFINITY;
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void scores_softmax_kernel(const float* __rest
   const int t_last = min(q_slices - 1, (min(i0 + kScoreRows, nq) - 1) / sq);
   for (int dt = 0; dt < 2 && t_first + dt <= t_last; ++dt) {
     unsigned* g = hist + ((int64_t)h * q_slices + t_first + dt) * kHistBins;
-    for (int bn = tid; bn < kHistBins; bn += blockDim.x) {
+    for (int bn = tid; bn < kHistBins; bn += kScoreThreads) {
       const unsigned c = lhist[dt * kHistBins + bn];
       if (c) atomicAdd(&g[bn], c);
     }
@@ -549,8 +549,8 @@ int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream)
 }
 
 size_t scores_smem_bytes(int nk, int s) {
-  static_assert(kKeyChunk * kKStride * sizeof(float) >= 2 * kHistBins * sizeof(unsigned), "histograms alias ks");
-  return sizeof(float) * ((size_t)kScoreRows * (kHeadDim + nk) + (size_t)kKeyChunk * kKStride) +
+  static_assert(2 * kKeyChunk * kKStride * sizeof(float) >= 2 * kHistBins * sizeof(unsigned), "histograms alias ks");
+  return sizeof(float) * ((size_t)kScoreRows * (kHeadDim + nk) + (size_t)2 * kKeyChunk * kKStride) +
          (size_t)kScoreRows * std::min(s, nk);
 }
 
@@ -563,7 +563,7 @@ int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int hea
   const size_t smem = scores_smem_bytes(nk, s);
   if (smem > 160 * 1024)
     return set_error(FVSR_ERR_UNSUPPORTED, "scores stage: too many key blocks for LDS");
-  hipLaunchKernelGGL(scores_softmax_kernel, grid, dim3(256), smem, stream, pq, pk, kmap, C, nq,
+  hipLaunchKernelGGL(scores_softmax_kernel, grid, dim3(kScoreThreads), smem, stream, pq, pk, kmap, C, nq,
                      nk, s, local, probs, hist, q_slices);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;

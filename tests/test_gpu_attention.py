@@ -294,3 +294,34 @@ def test_c4_iid_workload_subset(dev):
         assert (ov[b, :, h] == 0).all()
     full = [tuple(x) for x in np.argwhere(kc > 0)[:: max(1, int((kc > 0).sum()) // 12)]]
     assert _rows_vs_oracle(q, k, v, mask.cpu().numpy(), wl.heads, o, full) <= BF16_REL
+
+
+
+@pytest.mark.parametrize("density", [1.0, 0.6])
+def test_reference_raise_on_sharp_scores(dev, density):
+    """Scores that grow along the walk far past the first tile's max: key block j is scaled by s_j (0.05 .. 8), so a
+    row's logits span about 90 in log2 units and the reference is raised several times per row (each raise rescales
+    O and l and recomputes the tile). The scores are scaled in fp32 (a bf16-rounded prescaled Q would misplace the
+    dominant weights by up to 2^0.2 at these magnitudes). bf16 within its bar of the float64 oracle; the kernel
+    equal to the dense fallback (which raises at the same tiles) and to the list entry point, bit for bit."""
+    heads, lqb, nkb = 2, 3, 6
+    gen = torch.Generator().manual_seed(77)
+    scale = torch.tensor([0.05, 0.5, 2.0, 4.0, 6.0, 8.0]).repeat_interleave(128).view(-1, 1)
+    q = (3.0 * torch.randn((lqb * 128, heads * 128), generator=gen)).to(torch.bfloat16)
+    k = (scale * torch.randn((nkb * 128, heads * 128), generator=gen)).to(torch.bfloat16)
+    v = torch.randn((nkb * 128, heads * 128), generator=gen).to(torch.bfloat16)
+    m = (torch.rand((heads, lqb, nkb), generator=gen) < density).float()
+    m[:, :, 0] = 1.0                          # every row starts on the flat block
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), m.to(dev)
+    o = fvsr_lcsa.kernel_block_attention(qd, kd, vd, md, heads)
+    od = fvsr_lcsa.block_masked_attention(qd, kd, vd, md, heads)
+    kidx, kcnt = O.block_lists(m.numpy())
+    ol = fvsr_lcsa.block_sparse_attention(qd, kd, vd, torch.from_numpy(kidx).to(dev), torch.from_numpy(kcnt).to(dev),
+                                          heads)
+    torch.cuda.synchronize()
+    assert torch.equal(o, od)
+    assert torch.equal(o, ol)
+    ref = O.block_masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), m.numpy(), heads)
+    rel = _rel(o, ref)
+    print(f"  density {density}: rel {rel:.2e}", flush=True)
+    assert rel <= BF16_REL
