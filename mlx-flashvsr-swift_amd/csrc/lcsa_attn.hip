@@ -485,9 +485,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         };
         const i16x4 ax = aext(valid_next);
         float sum[QG][2];
-#pragma unroll
-        for (int q = 0; q < QG; ++q) sum[q][0] = sum[q][1] = 0.f;
-        float x_even = 0.f;
+        float xv[2];   // the exponentials of the last two micro-rounds
         auto micro = [&](auto i_c) {
           constexpr int I = decltype(i_c)::value;
           if constexpr (I == 0) {
@@ -512,17 +510,21 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
               mfma_acc(acc[w - QG][c & 3], vv, p_prev[w - QG][c >> 2]);
             }
           }
-          if constexpr (I < 16 * QG) {
-            // S(T) entry idx of group q; fp32 sums (v_dot2 would wait for the matrix core)
-            constexpr int q = I >> 4, idx = I & 15;
-            const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[q][idx], c_scale, negm[q]));
-            if constexpr ((I & 1) == 0) {
-              x_even = x;
-            } else {
-              p_cur[q][idx >> 3][(idx & 7) - 1] = (bf16)x_even;
-              p_cur[q][idx >> 3][idx & 7] = (bf16)x;
-              sum[q][(idx >> 1) & 1] += x_even + x;
+          // exponential I of S(T) (entry idx of group q); the exponential of the micro-round before is summed (fp32
+          // sums: v_dot2 would wait for the matrix core) and, completing a pair, packed to bf16 here, a micro-round
+          // after it was issued, so no wait state follows the transcendental
+          if constexpr (I >= 1 && I <= 16 * QG) {
+            constexpr int J = I - 1, qj = J >> 4, ij = J & 15;
+            if constexpr (ij < 2) sum[qj][ij] = xv[J & 1];
+            else sum[qj][ij & 1] += xv[J & 1];
+            if constexpr ((J & 1) == 1) {
+              p_cur[qj][ij >> 3][(ij & 7) - 1] = (bf16)xv[0];
+              p_cur[qj][ij >> 3][ij & 7] = (bf16)xv[1];
             }
+          }
+          if constexpr (I < 16 * QG) {
+            constexpr int q = I >> 4, idx = I & 15;
+            xv[I & 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[q][idx], c_scale, negm[q]));
           }
           if constexpr ((I & 3) == 1 && I / 4 < kDmaStep) dma(std::integral_constant<int, I / 4>{});
           __builtin_amdgcn_sched_barrier(0);
@@ -533,7 +535,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 #pragma unroll
         for (int q = 0; q < QG; ++q) {
           part[q] = sum[q][0] + sum[q][1];
-          grow |= !(pair_max(part[q]) <= kGrowSum);   // also inf / NaN
+          grow |= !(part[q] <= kGrowSum);   // either half of a row; also inf / NaN
         }
         if (__ballot(grow) != 0) {
           // raise the reference of the rows that grew to their max in S(T); the other rows keep theirs (their
