@@ -647,7 +647,11 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 // (workgroups b with b % 8 == x, dispatch is round-robin over the XCDs) holds positions x, x + 8, .. of the wave:
 // one contiguous range of rows, whose key lists overlap, so the XCD's L2 serves the key blocks they share.
 // next_dealt_item hands the positions out per XCD. The order does not affect results. Scans are wave-wide
-// (shuffles) with one step across the waves.
+// (shuffles) with one step across the waves. Up to kOrderLdsRows rows the lengths' bins and the sorted order stay in
+// LDS (kcnt is read once, the dealt order written once) and, while the waves' bitmaps fit together, every wave is
+// ranked in one pass (one bitmap segment per wave, one scan); beyond, the sorted order is staged in `order` itself
+// and the waves are ranked one after another.
+constexpr int kOrderLdsRows = 8192;
 __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
                                                           int dense, int grid, int32_t* __restrict__ order,
                                                           int32_t* __restrict__ counters) {
@@ -658,7 +662,11 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
   __shared__ __attribute__((aligned(16))) int first[kMaxPersistentWgs];   // one wave; padded with INT_MAX
   __shared__ unsigned bm[kWords];
   __shared__ int wpre[kWords];                                            // set bits in the words before word w
+  __shared__ int lord[kOrderLdsRows];                                     // the sorted order (rows <= kOrderLdsRows)
+  __shared__ uint8_t lbin[kOrderLdsRows];                                 // each row's bin (rows <= kOrderLdsRows)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool in_lds = rows <= kOrderLdsRows;
+  int* const sorted = in_lds ? lord : order;
   if (tid < kBins) bin_start[tid] = 0;
   __syncthreads();
   auto bin_of = [&](int r) -> int {   // bin 0 = the longest lists
@@ -666,7 +674,11 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
     const int len = c <= 0 ? 0 : (dense ? 1 : min((min(c, nk_stride) + 7) >> 3, kBins - 1));
     return kBins - 1 - len;
   };
-  for (int r = tid; r < rows; r += 1024) atomicAdd(&bin_start[bin_of(r)], 1);
+  for (int r = tid; r < rows; r += 1024) {
+    const int bn = bin_of(r);
+    if (in_lds) lbin[r] = (uint8_t)bn;
+    atomicAdd(&bin_start[bn], 1);
+  }
   __syncthreads();
   // exclusive scan of the 256 bin counts by waves 0..3
   {
@@ -681,63 +693,90 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
     }
   }
   __syncthreads();
-  for (int r = tid; r < rows; r += 1024) order[atomicAdd(&bin_start[bin_of(r)], 1)] = r;
+  for (int r = tid; r < rows; r += 1024) sorted[atomicAdd(&bin_start[in_lds ? (int)lbin[r] : bin_of(r)], 1)] = r;
   __threadfence_block();
   __syncthreads();
   grid = min(grid, kMaxPersistentWgs);
-  const bool use_bitmap = rows <= kWords * 32;
-  const int words = use_bitmap ? (rows + 31) / 32 : 0;
-  for (int w0 = 0; w0 < rows; w0 += grid) {
-    const int nw = min(grid, rows - w0);
-    for (int i = tid; i < kMaxPersistentWgs; i += 1024) first[i] = i < nw ? order[w0 + i] : 0x7fffffff;
-    for (int w = tid; w < words; w += 1024) bm[w] = 0u;
-    __syncthreads();
-    // rank of each row of the wave among them by row id: a bitmap over the row ids and a scan of its per-word
-    // popcounts; beyond 32 x 4096 rows, a scan of the wave's rows themselves
-    if (use_bitmap) {
-      for (int i = tid; i < nw; i += 1024) atomicOr(&bm[first[i] >> 5], 1u << (first[i] & 31));
-      __syncthreads();
-      int c[4], csum = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int w = 4 * tid + i;
-        c[i] = w < words ? __popc(bm[w]) : 0;
-        csum += c[i];
-      }
-      const int incl = (int)wave_incl_scan((unsigned)csum);
-      if (lane == 63) wtot[wave] = incl;
-      __syncthreads();
-      int run = incl - csum;
-      for (int w = 0; w < wave; ++w) run += wtot[w];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (4 * tid + i < words) wpre[4 * tid + i] = run;
-        run += c[i];
-      }
-      __syncthreads();
+  // position p of the sorted order goes to wave p / grid; XCD x holds m_x = (nw - x + 7) / 8 positions x, x + 8, ..
+  // of a wave of nw items, and ranks s_x .. s_x + m_x - 1 (by row id) go to it
+  auto deal = [&](int w0, int nw, int rank, int r) {
+    int x = 0, s0 = 0;
+    while (s0 + (nw - x + kXcds - 1) / kXcds <= rank) {
+      s0 += (nw - x + kXcds - 1) / kXcds;
+      ++x;
     }
-    const int n4 = (nw + 31) / 32 * 8;   // int4 groups to scan, a multiple of the unroll
-    for (int i = tid; i < nw; i += 1024) {
-      const int r = first[i];
-      int rank = 0;   // rows are distinct: ranks are a permutation of 0 .. nw - 1
+    order[w0 + (rank - s0) * kXcds + x] = r;
+  };
+  // exclusive scan of the popcounts of bm[0 .. n) into wpre (4 words per thread, n <= kWords)
+  auto scan_words = [&](int n) {
+    int c[4], csum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = 4 * tid + i;
+      c[i] = w < n ? __popc(bm[w]) : 0;
+      csum += c[i];
+    }
+    const int incl = (int)wave_incl_scan((unsigned)csum);
+    if (lane == 63) wtot[wave] = incl;
+    __syncthreads();
+    int run = incl - csum;
+    for (int w = 0; w < wave; ++w) run += wtot[w];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (4 * tid + i < n) wpre[4 * tid + i] = run;
+      run += c[i];
+    }
+    __syncthreads();
+  };
+  const int rwords = (rows + 31) / 32;
+  const int nwaves = (rows + grid - 1) / grid;
+  if (in_lds && nwaves * rwords <= kWords) {
+    // every wave at once: wave w's rows set their bits in bitmap segment w, one scan covers all segments
+    for (int i = tid; i < nwaves * rwords; i += 1024) bm[i] = 0u;
+    __syncthreads();
+    for (int p = tid; p < rows; p += 1024) {
+      const int r = sorted[p];
+      atomicOr(&bm[(p / grid) * rwords + (r >> 5)], 1u << (r & 31));
+    }
+    __syncthreads();
+    scan_words(nwaves * rwords);
+    for (int p = tid; p < rows; p += 1024) {
+      const int r = sorted[p], w = p / grid, wi = w * rwords + (r >> 5);
+      const int rank = wpre[wi] - wpre[w * rwords] + __popc(bm[wi] & ((1u << (r & 31)) - 1u));
+      deal(w * grid, min(grid, rows - w * grid), rank, r);
+    }
+  } else {
+    const bool use_bitmap = rows <= kWords * 32;
+    const int words = use_bitmap ? rwords : 0;
+    for (int w0 = 0; w0 < rows; w0 += grid) {
+      const int nw = min(grid, rows - w0);
+      for (int i = tid; i < kMaxPersistentWgs; i += 1024) first[i] = i < nw ? sorted[w0 + i] : 0x7fffffff;
+      for (int w = tid; w < words; w += 1024) bm[w] = 0u;
+      __syncthreads();
+      // rank of each row of the wave among them by row id: a bitmap over the row ids and a scan of its per-word
+      // popcounts; beyond 32 x 4096 rows, a scan of the wave's rows themselves
       if (use_bitmap) {
-        rank = wpre[r >> 5] + __popc(bm[r >> 5] & ((1u << (r & 31)) - 1u));
-      } else {
+        for (int i = tid; i < nw; i += 1024) atomicOr(&bm[first[i] >> 5], 1u << (first[i] & 31));
+        __syncthreads();
+        scan_words(words);
+      }
+      const int n4 = (nw + 31) / 32 * 8;   // int4 groups to scan, a multiple of the unroll
+      for (int i = tid; i < nw; i += 1024) {
+        const int r = first[i];
+        int rank = 0;   // rows are distinct: ranks are a permutation of 0 .. nw - 1
+        if (use_bitmap) {
+          rank = wpre[r >> 5] + __popc(bm[r >> 5] & ((1u << (r & 31)) - 1u));
+        } else {
 #pragma unroll 8
-        for (int j = 0; j < n4; ++j) {
-          const int4 f = reinterpret_cast<const int4*>(first)[j];
-          rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+          for (int j = 0; j < n4; ++j) {
+            const int4 f = reinterpret_cast<const int4*>(first)[j];
+            rank += (f.x < r) + (f.y < r) + (f.z < r) + (f.w < r);
+          }
         }
+        deal(w0, nw, rank, r);
       }
-      // XCD x holds m_x = (nw - x + 7) / 8 positions x, x + 8, ..; ranks s_x .. s_x + m_x - 1 go to it
-      int x = 0, s0 = 0;
-      while (s0 + (nw - x + kXcds - 1) / kXcds <= rank) {
-        s0 += (nw - x + kXcds - 1) / kXcds;
-        ++x;
-      }
-      order[w0 + (rank - s0) * kXcds + x] = r;
+      __syncthreads();
     }
-    __syncthreads();
   }
   // queue y's counter starts past the first wave (the workgroups take it without the counters)
   if (tid < kXcds) counters[8 * tid] = (grid - tid + kXcds - 1) / kXcds;
