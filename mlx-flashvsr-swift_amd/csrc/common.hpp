@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "../../include/fvsr_lcsa.h"
 
@@ -45,6 +46,15 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   const int xcd = bid % kXcds, idx = bid / kXcds;
   const int q = nwg / kXcds, rem = nwg % kXcds;
   return xcd < rem ? xcd * (q + 1) + idx : rem * (q + 1) + (xcd - rem) * q + idx;
+}
+
+// f(integral_constant<I>) for I = B .. E-1, unrolled at compile time
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 // inclusive scan over the 64 lanes of a wave

@@ -64,15 +64,6 @@ __device__ __forceinline__ float rescale_if_grown(float mxc, float& m_run, float
   return m_run == -INFINITY ? 0.f : m_run;
 }
 
-// f(integral_constant<I>) for I = B .. E-1, unrolled at compile time
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
 // ------------------------------------------------------------------------------------------------------------
 // bf16
 // ------------------------------------------------------------------------------------------------------------

@@ -109,6 +109,7 @@ __device__ __forceinline__ void wave_hist_add(unsigned* h, unsigned key, bool va
 constexpr int kScoreRows = 8;   // query blocks per workgroup (one per wave in the softmax)
 constexpr int kScoreThreads = 512;   // 8 waves: two halves of 4 stage alternate key chunks side by side
 constexpr int kKeyChunk = 64;   // key blocks staged in LDS at a time by one half
+constexpr int kChunksInFlight = 2;   // chunk loads each half keeps in flight (registers)
 constexpr int kKStride = kHeadDim + 4;   // padded LDS row of a pooled key (floats)
 constexpr int kHistBins = 4096; // top-12-bit bins (bits 30..19) of the prob bit patterns
 
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
     qa[t + 3] = x[3];
   }
   // one round: each half stages its chunk (j0 < nk) and multiplies it; both halves take part in the barriers
-  auto chunk = [&](f32x4 (&pre)[kLoads], int j0) {
+  auto chunk = [&](f32x4 (&pre)[kLoads], int j0, int j_next) {
     const int nj = j0 < nk ? min(kKeyChunk, nk - j0) : 0;
     __syncthreads();   // the previous round's rows have been read
 #pragma unroll
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
       if (jj < nj) *(f32x4*)(kst + jj * kKStride + 4 * c4) = pre[i];
     }
     __syncthreads();
-    if (j0 + 2 * kKeyChunk < nk) load_chunk(pre, j0 + 2 * kKeyChunk);
+    if (j_next < nk) load_chunk(pre, j_next);
     if (16 * hw < nj) {   // wave-uniform; rows of keys past nj hold stale data and are not stored
       const float* krow = kst + (16 * hw + li) * kKStride + 32 * lg;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -210,9 +211,21 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
       }
     }
   };
-  f32x4 pre[kLoads];
-  load_chunk(pre, half * kKeyChunk);
-  for (int j0 = 0; j0 < nk; j0 += 2 * kKeyChunk) chunk(pre, j0 + half * kKeyChunk);
+  // round r: half h multiplies chunk 2 r + h; each half keeps the chunks of its next kChunksInFlight rounds in flight
+  // (a register ring), so a round waits on loads issued that many rounds before
+  f32x4 pre[kChunksInFlight][kLoads];
+  const int rounds = (nk + 2 * kKeyChunk - 1) / (2 * kKeyChunk);
+  auto chunk_of = [&](int r) { return (2 * r + half) * kKeyChunk; };
+  static_for<0, kChunksInFlight>([&](auto d_c) {
+    constexpr int D = decltype(d_c)::value;
+    if (chunk_of(D) < nk) load_chunk(pre[D], chunk_of(D));
+  });
+  for (int r0 = 0; r0 < rounds; r0 += kChunksInFlight) {
+    static_for<0, kChunksInFlight>([&](auto d_c) {
+      constexpr int D = decltype(d_c)::value;
+      if (r0 + D < rounds) chunk(pre[D], chunk_of(r0 + D), chunk_of(r0 + D + kChunksInFlight));   // uniform
+    });
+  }
   __syncthreads();
   for (int e = tid; e < 2 * kHistBins; e += kScoreThreads) lhist[e] = 0u;
   __syncthreads();
@@ -277,6 +290,7 @@ constexpr int kThrParts = 16;           // workgroups per (head, query slice) ro
 constexpr int kThrThreads = 256;
 constexpr int kThrLdsCand = 16384;      // candidates the last workgroup holds in LDS
 constexpr int kCandPerBlock = 128;      // candidate words of the workspace per (head, query block)
+constexpr int kThrRegs = 16;            // elements per thread held in registers (a share of up to 4096)
 
 // per-row control words after the histograms: [0] candidates gathered, [1] workgroups arrived
 __device__ __forceinline__ unsigned* thr_ctl(unsigned* hist12, int rows, int row) {
@@ -406,8 +420,22 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
   if (gather) {
     const int64_t per = (n + kThrParts - 1) / kThrParts;
     const int64_t e0 = part * per, e1 = min<int64_t>(n, e0 + per);
+    // a share of up to kThrRegs * kThrThreads elements is loaded into registers once (every load in flight at the
+    // same time) and both counted and gathered from there; a larger share is read twice
+    const bool in_regs = per <= (int64_t)kThrRegs * kThrThreads;
+    unsigned rv[kThrRegs];
     unsigned mine = 0;
-    for (int64_t e = e0 + tid; e < e1; e += kThrThreads) mine += (bits[e] >> 19) == bin ? 1u : 0u;
+    if (in_regs) {
+#pragma unroll
+      for (int i = 0; i < kThrRegs; ++i) {
+        const int64_t e = e0 + tid + (int64_t)i * kThrThreads;
+        rv[i] = e < e1 ? bits[e] : 0xffffffffu;   // all-ones: outside every bin of a prob in [0, 1]
+      }
+#pragma unroll
+      for (int i = 0; i < kThrRegs; ++i) mine += (rv[i] >> 19) == bin ? 1u : 0u;
+    } else {
+      for (int64_t e = e0 + tid; e < e1; e += kThrThreads) mine += (bits[e] >> 19) == bin ? 1u : 0u;
+    }
     const unsigned minc = wave_incl_scan(mine);
     if (lane == 63) wsum[wave] = minc;
     __syncthreads();
@@ -421,14 +449,25 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
                                                                 __HIP_MEMORY_SCOPE_AGENT) : 0u;
     __syncthreads();
     unsigned at = s_arrived + off;
-    if (mine)
-      for (int64_t e = e0 + tid; e < e1; e += kThrThreads) {
-        const unsigned u = bits[e];
-        if ((u >> 19) == bin) {
-          if (at < cap) __hip_atomic_store(cw + at, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ++at;
+    if (mine) {
+      if (in_regs) {
+#pragma unroll
+        for (int i = 0; i < kThrRegs; ++i) {
+          if ((rv[i] >> 19) == bin) {
+            if (at < cap) __hip_atomic_store(cw + at, rv[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ++at;
+          }
+        }
+      } else {
+        for (int64_t e = e0 + tid; e < e1; e += kThrThreads) {
+          const unsigned u = bits[e];
+          if ((u >> 19) == bin) {
+            if (at < cap) __hip_atomic_store(cw + at, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ++at;
+          }
         }
       }
+    }
     __syncthreads();   // every thread has read s_arrived
   }
   FVSR_WAIT_VM0();   // this wave's candidates are stored at device scope
