@@ -162,9 +162,13 @@ __device__ __forceinline__ int next_dealt_item(int32_t* counters, int rows) {
 }
 
 // LDS operand requests of chunk / pair j >= 2 (j = 0, 1: micro-round 0), in micro-rounds of a step with QG query
-// groups per wave: 7 (QG 2) or 4 (QG 1) micro-rounds before the QK MFMA that uses them
-template <int QG>
-constexpr int attn_read_at(int j) { return QG + 2 * QG * j - (QG == 2 ? 7 : 4); }
+// groups per wave and EXT mask MFMAs ahead of the first QK chunk: 7 (QG 2) or 4 (QG 1) micro-rounds before the QK
+// MFMA that uses them, micro-round 0 at the earliest
+template <int QG, int EXT>
+constexpr int attn_read_at(int j) {
+  const int r = EXT + 2 * QG * j - (QG == 2 ? 7 : 4);
+  return r > 0 ? r : 0;
+}
 
 template <bool DENSE, int QG>
 __global__ __attribute__((amdgpu_flat_work_group_size(256 / QG, 256 / QG), amdgpu_waves_per_eu(3 - QG, 3 - QG)))
@@ -330,6 +334,17 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   auto mfma_ext = [&](const i16x4& ax, const i16x4& bx) -> f32x16 {
     return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ax, bx, f32x16{}, 0, 0, 0);
   };
+  // The sparse walk lists selected blocks only, so its tiles are whole (32 keys) but for a ragged last block, a listed
+  // index outside [0, nk) and the tile past the end of the walk, whose rows all load as zeros. It starts S at zero
+  // (no mask MFMA) and, on a tile with fewer than 32 keys taking part (a wave-uniform branch), sets the scores of the
+  // keys at or past `valid` to -2^100 afterwards: the values the mask MFMA gives there (their K rows are zeros).
+  // Lane element i of a 32 x 32 MFMA result is key row 8 (i / 4) + 4 g + i % 4.
+  auto mask_tile = [&](f32x16& s, int valid) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 8 * (i >> 2) + 4 * g + (i & 3) >= valid ? kMaskedScore : s[i];
+  };
+  // mask MFMAs per step: the dense walk's tiles mix selected and unselected blocks
+  constexpr int kExt = DENSE ? QG : 0;
   lds_char* const lds = (lds_char*)(uintptr_t)smem_lds;
   // S^T = K Q^T (keys that do not take part: - 2^100) for both groups, K from ring slot SLOT
   auto qk = [&](auto slot_c, int valid, f32x16 (&s)[QG]) {
@@ -337,13 +352,20 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     bf16x8 kk[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) kk[t] = *(const lds_bf16x8*)(lds + SLOT * kTileBytes + k_off[t]);
-    const i16x4 ax = aext(valid);
+    if constexpr (DENSE) {
+      const i16x4 ax = aext(valid);
 #pragma unroll
-    for (int q = 0; q < QG; ++q) s[q] = mfma_ext(ax, bext);
+      for (int q = 0; q < QG; ++q) s[q] = mfma_ext(ax, bext);
+    }
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int q = 0; q < QG; ++q) s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[t], qop[q][t], s[q], 0, 0, 0);
+      for (int q = 0; q < QG; ++q)
+        s[q] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[t], qop[q][t], (DENSE || t > 0) ? s[q] : f32x16{}, 0, 0, 0);
+    if (!DENSE && valid < kTileKeys) {
+#pragma unroll
+      for (int q = 0; q < QG; ++q) mask_tile(s[q], valid);
+    }
   };
   // O^T += V^T P^T, V from ring slot SLOT
   auto pv = [&](auto slot_c, const bf16x8 (&p)[QG][2]) {
@@ -451,13 +473,14 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 #pragma unroll
         for (int q = 0; q < QG; ++q) m_row[q] = fmaxf(m_row[q], row_max(s_cur[q]));
       } else {
-        // 17 * QG micro-rounds, one MFMA each, fenced so the order below is the issue order. A wave issues in order
-        // and an MFMA occupies the matrix core for 32 cycles: every MFMA is followed by a slice of the other work,
-        // which issues while it runs (MFMAs grouped back to back would leave that work unoverlapped). MFMA order: the
-        // reference / mask MFMA of QK(T+1) for each query group, then for c = 0..7 QK chunk c (each group) and PV
-        // pair c (each group). Slices: exponential I of S(T) in micro-round I (pairs packed to bf16 and summed on odd
-        // I); the LDS operands of chunk / pair j requested at least 4 micro-rounds before use (attn_read_at); one of
-        // the step's buffer->LDS copies every 4 micro-rounds.
+        // 16 * QG micro-rounds with one MFMA each (17 * QG in the dense walk), fenced so the order below is the
+        // issue order, then one more for the last exponential. A wave issues in order and an MFMA occupies the
+        // matrix core for 32 cycles: every MFMA is followed by a slice of the other work, which issues while it runs
+        // (MFMAs grouped back to back would leave that work unoverlapped). MFMA order: (dense walk) the mask MFMA of
+        // QK(T+1) for each query group, then for c = 0..7 QK chunk c (each group) and PV pair c (each group).
+        // Slices: exponential I of S(T) in micro-round I (pairs packed to bf16 and summed a micro-round later); the
+        // LDS operands of chunk / pair j requested up to 4 micro-rounds before use (attn_read_at); one of the step's
+        // buffer->LDS copies every 4 micro-rounds.
         lds_char* const vbase = lds + kVRing + ((SUB + 3) & 3) * kTileBytes;
         lds_char* const kbase = lds + ((SUB + 1) & 3) * kTileBytes;
         i16x4 va[8], vb[8];
@@ -474,7 +497,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           if constexpr (R < kDmaK) dma_k(KS{}, std::integral_constant<int, R>{}, soff_k);
           else dma_v(VS{}, std::integral_constant<int, R - kDmaK>{}, soff_v);
         };
-        const i16x4 ax = aext(valid_next);
+        i16x4 ax{};
+        if constexpr (DENSE) ax = aext(valid_next);
         float sum[QG][2];
         float xv[2];   // the exponentials of the last two micro-rounds
         auto micro = [&](auto i_c) {
@@ -485,14 +509,17 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           }
           static_for<2, 8>([&](auto j_c) {
             constexpr int J = decltype(j_c)::value;
-            if constexpr (attn_read_at<QG>(J) == I) read_ops(J);
+            if constexpr (attn_read_at<QG, kExt>(J) == I) read_ops(J);
           });
-          if constexpr (I < QG) {
+          if constexpr (I < kExt) {
             s_nxt[I] = mfma_ext(ax, bext);
-          } else {
-            constexpr int c = (I - QG) / (2 * QG), w = (I - QG) % (2 * QG);
+          } else if constexpr (I < kExt + 16 * QG) {
+            constexpr int c = (I - kExt) / (2 * QG), w = (I - kExt) % (2 * QG);
             if constexpr (w < QG) {
-              s_nxt[w] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[c], qop[w][c], s_nxt[w], 0, 0, 0);
+              if constexpr (DENSE || c > 0)
+                s_nxt[w] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[c], qop[w][c], s_nxt[w], 0, 0, 0);
+              else
+                s_nxt[w] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kk[0], qop[w][0], f32x16{}, 0, 0, 0);
             } else {
               // whole-vector concatenation: element-wise assembly of the operand is mis-lowered (one dword
               // duplicated)
@@ -520,7 +547,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           if constexpr ((I & 3) == 1 && I / 4 < kDmaStep) dma(std::integral_constant<int, I / 4>{});
           __builtin_amdgcn_sched_barrier(0);
         };
-        static_for<0, 17 * QG>(micro);
+        static_for<0, kExt + 16 * QG + (DENSE ? 0 : 1)>(micro);
         float part[QG];
         bool grow = false;
 #pragma unroll
@@ -560,6 +587,11 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         for (int q = 0; q < QG; ++q) {
           l_run[q] += part[q];
           part_max[q] = fmaxf(part_max[q], part[q]);
+        }
+        // last in the step: a branch before the row sums would let the compiler sink the exponentials past it
+        if (!DENSE && valid_next < kTileKeys) {
+#pragma unroll
+          for (int q = 0; q < QG; ++q) mask_tile(s_nxt[q], valid_next);
         }
       }
       // keep every instruction of this step on its side of the barrier
