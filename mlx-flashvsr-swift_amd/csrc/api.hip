@@ -37,7 +37,7 @@ int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices
 int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int C, int t0,
                         const void* wq, const void* wk, float eps, const float* rope, void* q_out, void* k_out,
                         void* v_out, int dst_slot0, int capacity, int slice_blocks, hipStream_t stream);
-int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream);
+int launch_pool_mean(int dtype, PoolMean* jobs, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream);
 int launch_pool_finish(const PoolDst* dst, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream);
 int rope_table_floats();
 int blas_create(int device, void** out);
@@ -67,7 +67,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // workspace carve for one select + attention call
 struct Carve {
-  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, partial, hist, cand, total;
+  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, hist, cand, total;
 };
 static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   Carve c;
@@ -81,7 +81,6 @@ static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   c.order = off; off += align256((size_t)heads * nq * 4);
   c.counter = off; off += 256;
   c.thr = off; off += align256((size_t)heads * nq * 4);   // per (head, query slice) thresholds (nq >= slices)
-  c.partial = off; off += align256((size_t)(nq + nk) * kPoolParts * C * 4);   // pooling runs of Q, then K
   c.hist = off; off += align256(hist12_bytes(heads, (int)nq));   // nq >= query slices
   c.cand = off; off += align256(topk_cand_bytes(heads, nq));
   c.total = off;
@@ -253,27 +252,16 @@ static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, con
   float* probs = probs_out ? probs_out : (float*)(ws + cv.probs);
   uint8_t* sel = sel_out ? sel_out : (uint8_t*)(ws + cv.sel);
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
-  float* partial = (float*)(ws + cv.partial);
   unsigned* hist = (unsigned*)(ws + cv.hist);
   const float* pk = pk_ready ? pk_src : (const float*)(ws + cv.pk);
   if (!q_pooled || !pk_ready) {
-    // block sums of Q (and K) in one launch, then the block means and the histogram reset in one more
-    PoolSrc src[2];
-    PoolDst dst[2];
+    // block means of Q (and K) and the histogram reset, one launch
+    PoolMean jobs[2];
     int n = 0;
-    float* kpart = partial + (size_t)nq * kPoolParts * C;
-    if (!q_pooled) {
-      src[n] = PoolSrc{qW, partial, lq, 0};
-      dst[n++] = PoolDst{partial, pq, lq, 0, 0, 1, 1 << 30};
-    }
-    if (!pk_ready) {
-      src[n] = PoolSrc{kW, kpart, lk, 0};
-      dst[n++] = PoolDst{kpart, (float*)(ws + cv.pk), lk, 0, 0, 1, 1 << 30};
-    }
-    if ((rc = launch_pool_parts(dtype, src, n, C, stream))) return rc;
-    for (int i = 0; i < n; ++i) dst[i].nb = src[i].nb;
-    if ((rc = launch_pool_finish(dst, n, C, q_pooled ? nullptr : hist,
-                                 (int64_t)(hist12_bytes(heads, q_slices) / sizeof(unsigned)), stream)))
+    if (!q_pooled) jobs[n++] = PoolMean{qW, lq, pq, 0, 0, 1, 1 << 30};
+    if (!pk_ready) jobs[n++] = PoolMean{kW, lk, (float*)(ws + cv.pk), 0, 0, 1, 1 << 30};
+    if ((rc = launch_pool_mean(dtype, jobs, n, C, q_pooled ? nullptr : hist,
+                               (int64_t)(hist12_bytes(heads, q_slices) / sizeof(unsigned)), stream)))
       return rc;
   }
   if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, hist, q_slices, stream)))
@@ -559,13 +547,13 @@ int fvsr_kv_ring_append(fvsr_kv_ring* r, int layer, const void* k_new, const voi
 
 }  // extern "C"
 
-// The ring append of fvsr_kv_ring_append_qkv. With q_pool set (the layer call), the block sums of the written
-// queries ride in the same pool_part launch as the new keys' (q_pool->partial, its own scratch), their means go
-// to q_pooled in the same pool_finish launch, which also clears the selection histogram `hist` (nhist words).
+// The ring append of fvsr_kv_ring_append_qkv. With q_pooled set (the layer call), the block means of the written
+// queries ride in the same pooling launch as the new keys' (to q_pooled), which also clears the selection
+// histogram `hist` (nhist words).
 static int append_qkv_impl(fvsr_kv_ring* r, int layer, const void* q, const void* k, const void* v, int n_slices,
                            int t0, const void* norm_q_weight, const void* norm_k_weight, float eps,
-                           const float* rope_tables, void* q_out, hipStream_t stream, float* q_partial = nullptr,
-                           float* q_pooled = nullptr, unsigned* hist = nullptr, int64_t nhist = 0) {
+                           const float* rope_tables, void* q_out, hipStream_t stream, float* q_pooled = nullptr,
+                           unsigned* hist = nullptr, int64_t nhist = 0) {
   int rc = check_layer(r, layer);
   if (rc) return rc;
   FVSR_REQUIRE(n_slices > 0, FVSR_ERR_INVALID_ARG, "n_slices must be > 0");
@@ -583,24 +571,20 @@ static int append_qkv_impl(fvsr_kv_ring* r, int layer, const void* q, const void
                            norm_k_weight, eps, rope_tables, q_out, r->layer_k(layer), r->layer_v(layer), slot0,
                            r->capacity, r->s, stream);
   if (rc) return rc;
-  // pooled keys of the new slots, as for plain buffers: block sums over the slots up to the end of the ring, then
-  // the wrapped remainder from slot 0 (and the queries'), one launch
+  // pooled keys of the new slots, as for plain buffers: block means over the slots up to the end of the ring, then
+  // the wrapped remainder from slot 0 (and the queries' means, and the histogram reset), one launch
   const int first = std::min(n_slices, r->capacity - slot0);
   const size_t slot_bytes = (size_t)r->s * kBlock * r->C * esize(r->dtype);
   const int64_t lq = (int64_t)nb * kBlock;
-  PoolSrc src[3];
-  int ns = 0;
-  src[ns++] = PoolSrc{r->layer_k(layer) + slot0 * slot_bytes, r->partial, (int64_t)first * r->s * kBlock, 0};
+  PoolMean jobs[3];
+  int nj = 0;
+  jobs[nj++] = PoolMean{r->layer_k(layer) + slot0 * slot_bytes, (int64_t)first * r->s * kBlock,
+                        r->layer_pooled(layer), 0, slot0, r->capacity, r->s};
   if (first < n_slices)
-    src[ns++] = PoolSrc{r->layer_k(layer), r->partial + (size_t)first * r->s * kPoolParts * r->C,
-                        (int64_t)(n_slices - first) * r->s * kBlock, 0};
-  if (q_partial) src[ns++] = PoolSrc{q_out, q_partial, lq, 0};
-  if ((rc = launch_pool_parts(r->dtype, src, ns, r->C, stream))) return rc;
-  PoolDst dst[2];
-  int nd = 0;
-  dst[nd++] = PoolDst{r->partial, r->layer_pooled(layer), lq, nb, slot0, r->capacity, r->s};
-  if (q_partial) dst[nd++] = PoolDst{q_partial, q_pooled, lq, nb, 0, 1, 1 << 30};
-  if ((rc = launch_pool_finish(dst, nd, r->C, hist, nhist, stream))) return rc;
+    jobs[nj++] = PoolMean{r->layer_k(layer), (int64_t)(n_slices - first) * r->s * kBlock, r->layer_pooled(layer), 0,
+                          0, r->capacity, r->s};
+  if (q_pooled) jobs[nj++] = PoolMean{q_out, lq, q_pooled, 0, 0, 1, 1 << 30};
+  if ((rc = launch_pool_mean(r->dtype, jobs, nj, r->C, hist, nhist, stream))) return rc;
   r->count[layer] += n_slices;
   return FVSR_OK;
 }
@@ -764,7 +748,7 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* q
   const RingMark mark = ring_mark(r, layer);
   // the pooled queries and the histogram reset ride in the append's pooling launches
   if ((rc = append_qkv_impl(r, layer, q, k, v, n_new_slices, t0, norm_q_weight, norm_k_weight, eps, rope_tables,
-                            q_work, st, (float*)(ws + cv.partial), (float*)(ws + cv.pq), (unsigned*)(ws + cv.hist),
+                            q_work, st, (float*)(ws + cv.pq), (unsigned*)(ws + cv.hist),
                             (int64_t)(hist12_bytes(r->heads, q_slices) / sizeof(unsigned)))))
     return rc;
   const int nk = r->count[layer] * r->s;

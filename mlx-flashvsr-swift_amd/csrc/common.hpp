@@ -92,13 +92,14 @@ inline KeyMap make_key_map(int slot_head, int capacity, int slice_blocks) {
 }
 inline KeyMap plain_key_map() { return make_key_map(0, 1, 1 << 16); }
 
-// One block-pooling source of pool_part_kernel (lcsa_select.hip): the fp32 sums of the runs of 32 tokens of the L
-// tokens of x (nb = ceil(L / 128) blocks) go to partial[(b * kPoolParts + part) * C + c].
-struct PoolSrc {
+// One job of pool_mean_kernel (lcsa_select.hip): the block means of the L tokens of x (nb = ceil(L / 128) blocks);
+// block b is written to row ((slot0 + b / slice_blocks) % capacity) * slice_blocks + b % slice_blocks of out (a ring
+// slot mapping; slot0 0, capacity 1, slice_blocks >= nb for a plain buffer).
+struct PoolMean {
   const void* x;
-  float* partial;
   int64_t L;
-  int nb;
+  float* out;
+  int nb, slot0, capacity, slice_blocks;
 };
 
 // One block-mean target of pool_finish_kernel (kv_ring.hip): nb blocks (L tokens) of run sums in partial; block b

@@ -9,9 +9,10 @@
 //   k = min(n - 1, topk).
 //
 // Kernels (all HBM/L2-bound, no MFMA — the score product is 0.1 GFLOP):
-//   pool_part_kernel     one workgroup per run of 32 tokens of a block: coalesced 16-byte loads, fp32 sums (Q
-//                        and K, or Q and the new ring keys, in one launch); the means come from pool_finish_kernel
-//                        (kv_ring.hip) in a fixed order, which also clears the histogram below
+//   pool_mean_kernel     one workgroup per 128-token block (and run of up to 256 channel vectors): its four
+//                        quarters sum one run of 32 tokens each (coalesced 16-byte loads, fp32), the runs meet in
+//                        LDS and the block mean ((r0 + r1) + (r2 + r3)) / n is stored (Q and K, or Q and the new
+//                        ring keys, in one launch); the launch also clears the histogram below
 //   scores_softmax_kernel one 8-wave workgroup per (8 query blocks, head): pooled-key rows staged through LDS in
 //                         coalesced chunks of 64 keys, two chunks side by side, read once per 8 query rows; scores
 //                         + local mask in LDS, one wave per row for max / exp / sum / normalise; it also counts the
@@ -42,34 +43,46 @@ struct Vec16<bf16> {
   typedef bf16x8 type;
 };
 
-// Sources s0, s1, s2 ((L, C) tokens each) share one launch: grid (s0.nb + s1.nb + s2.nb, kPoolParts), block
-// index b of the grid runs over s0's blocks, then s1's, then s2's. Run `part` of block b sums rows
-// [b*128 + 32*part, +32) that exist into partial[(b * kPoolParts + part) * C + c] (fp32); pool_finish_kernel forms
-// the block means.
+// Jobs j0, j1, j2 share one launch: grid (j0.nb + j1.nb + j2.nb, ceil(nvec / per)) with `per` threads per quarter,
+// block index b of the grid runs over j0's blocks, then j1's, then j2's. Quarter `part` of the workgroup sums the
+// rows [b*128 + 32*part, +32) that exist, in row order, for channel vectors y*per .. y*per + per - 1; the mean is
+// ((r0 + r1) + (r2 + r3)) / n, the order the ring append's runs are finished in (pool_finish_kernel), so pooled keys
+// are bit-identical whichever path wrote them. Every workgroup also clears its share of `zero` (nzero words).
+constexpr int kPoolVecs = 256;   // channel vectors per workgroup quarter, at most
 template <typename T>
-__global__ void pool_part_kernel(PoolSrc s0, PoolSrc s1, PoolSrc s2, int C) {
+__global__ __launch_bounds__(kPoolParts * kPoolVecs) void pool_mean_kernel(PoolMean j0, PoolMean j1, PoolMean j2,
+                                                                          int C, unsigned* __restrict__ zero,
+                                                                          int64_t nzero) {
   constexpr int VN = Vec16<T>::N;
   constexpr int kRun = kBlock / kPoolParts;
   typedef typename Vec16<T>::type VT;
+  __shared__ float red[kPoolParts - 1][kPoolVecs][VN];   // runs 1..3; run 0 stays in registers
+  const int64_t nthreads = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+  for (int64_t e = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; e < nzero;
+       e += nthreads)
+    zero[e] = 0u;
   int b = blockIdx.x;
-  const int part = blockIdx.y;
-  PoolSrc src = s0;
-  if (b >= s0.nb) {
-    b -= s0.nb;
-    src = s1;
-    if (b >= s1.nb) {
-      b -= s1.nb;
-      src = s2;
+  PoolMean job = j0;
+  if (b >= j0.nb) {
+    b -= j0.nb;
+    job = j1;
+    if (b >= j1.nb) {
+      b -= j1.nb;
+      job = j2;
     }
   }
-  const T* __restrict__ x = (const T*)src.x;
-  const int64_t r0 = (int64_t)b * kBlock + part * kRun;
-  const int n = (int)max<int64_t>(0, min<int64_t>(kRun, src.L - r0));
+  if (b >= job.nb) return;   // a launch that only clears `zero`
+  const int per = blockDim.x / kPoolParts;   // threads per quarter
+  const int part = threadIdx.x / per, t = threadIdx.x - part * per;
+  const int cv = blockIdx.y * per + t;
   const int nvec = C / VN;
-  for (int cv = threadIdx.x; cv < nvec; cv += blockDim.x) {
-    float acc[VN];
+  const T* __restrict__ x = (const T*)job.x;
+  const int64_t r0 = (int64_t)b * kBlock + part * kRun;
+  const int n = (int)max<int64_t>(0, min<int64_t>(kRun, job.L - r0));
+  float acc[VN];
 #pragma unroll
-    for (int e = 0; e < VN; ++e) acc[e] = 0.f;
+  for (int e = 0; e < VN; ++e) acc[e] = 0.f;
+  if (cv < nvec) {
     const T* p = x + r0 * C + cv * VN;
 #pragma unroll 8
     for (int r = 0; r < n; ++r) {
@@ -77,10 +90,19 @@ __global__ void pool_part_kernel(PoolSrc s0, PoolSrc s1, PoolSrc s2, int C) {
 #pragma unroll
       for (int e = 0; e < VN; ++e) acc[e] += (float)v[e];
     }
-    float* o = src.partial + ((int64_t)b * kPoolParts + part) * C + cv * VN;
-#pragma unroll
-    for (int e = 0; e < VN; ++e) o[e] = acc[e];
   }
+  if (part > 0) {
+#pragma unroll
+    for (int e = 0; e < VN; ++e) red[part - 1][t][e] = acc[e];
+  }
+  __syncthreads();
+  if (part != 0 || cv >= nvec) return;
+  const float cnt = (float)min<int64_t>(kBlock, job.L - (int64_t)b * kBlock);
+  const int64_t db =
+      (int64_t)((job.slot0 + b / job.slice_blocks) % job.capacity) * job.slice_blocks + (b % job.slice_blocks);
+  float* o = job.out + db * C + cv * VN;
+#pragma unroll
+  for (int e = 0; e < VN; ++e) o[e] = ((acc[e] + red[0][t][e]) + (red[1][t][e] + red[2][t][e])) / cnt;
 }
 
 // Adds 1 to h[key] for every lane with `valid`; must be called by all 64 lanes of the wave together. Lanes with
@@ -564,25 +586,29 @@ __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict_
 // ------------------------------------------------------------------------------------------------------------
 // launch
 // ------------------------------------------------------------------------------------------------------------
-// the per-run block sums of n (1..3) sources in one launch; each source's nb is set here from its L
-int launch_pool_parts(int dtype, PoolSrc* src, int n, int C, hipStream_t stream) {
-  PoolSrc s[3] = {};
+// the block means of n (1..3) jobs in one launch (each job's nb is set here from its L); it also clears
+// zero[0 .. nzero) (zero may be null)
+int launch_pool_mean(int dtype, PoolMean* jobs, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream) {
+  PoolMean j[3] = {};
   int nb = 0;
   for (int i = 0; i < n && i < 3; ++i) {
-    s[i] = src[i];
-    s[i].nb = (int)ceil_div(std::max<int64_t>(0, s[i].L), kBlock);
-    src[i].nb = s[i].nb;
-    nb += s[i].nb;
+    j[i] = jobs[i];
+    j[i].nb = (int)ceil_div(std::max<int64_t>(0, j[i].L), kBlock);
+    jobs[i].nb = j[i].nb;
+    nb += j[i].nb;
   }
-  if (nb <= 0) return FVSR_OK;
+  if (!zero) nzero = 0;
+  if (nb <= 0 && nzero <= 0) return FVSR_OK;
   const int vn = dtype == FVSR_DTYPE_BF16 ? 8 : 4;
   const int nvec = C / vn;
-  const int threads = std::min(1024, ((nvec + 63) / 64) * 64);
-  const dim3 grid(nb, kPoolParts);
+  const int per = std::min(kPoolVecs, ((nvec + 63) / 64) * 64);   // threads per quarter
+  const dim3 grid(std::max(nb, 1), (unsigned)ceil_div(nvec, per));
   if (dtype == FVSR_DTYPE_BF16)
-    hipLaunchKernelGGL(pool_part_kernel<bf16>, grid, dim3(threads), 0, stream, s[0], s[1], s[2], C);
+    hipLaunchKernelGGL(pool_mean_kernel<bf16>, grid, dim3(kPoolParts * per), 0, stream, j[0], j[1], j[2], C, zero,
+                       nzero);
   else
-    hipLaunchKernelGGL(pool_part_kernel<float>, grid, dim3(threads), 0, stream, s[0], s[1], s[2], C);
+    hipLaunchKernelGGL(pool_mean_kernel<float>, grid, dim3(kPoolParts * per), 0, stream, j[0], j[1], j[2], C, zero,
+                       nzero);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }
@@ -593,8 +619,8 @@ size_t scores_smem_bytes(int nk, int s) {
          (size_t)kScoreRows * std::min(s, nk);
 }
 
-// hist: (heads * q_slices * kHistBins) u32 workspace, zeroed by the caller before the launch (pool_finish_kernel
-// clears it together with the pooled queries)
+// hist: (heads * q_slices * kHistBins) u32 workspace, zeroed by the caller before the launch (pool_mean_kernel
+// clears it while it pools the queries)
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
                           const uint8_t* local, float* probs, unsigned* hist, int q_slices, hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;

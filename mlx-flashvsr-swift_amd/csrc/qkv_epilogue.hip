@@ -17,8 +17,8 @@
 // Kernel: one wave per token (4 per workgroup), tokens in natural order so every wave reads three contiguous rows.
 // Each lane holds C / 64 / 8 vectors of 8 channels (bf16) of q, k and v; the sum of squares of a row is a wave
 // butterfly; every lane then normalises, weights and rotates its own channels and writes them to the token's window
-// position. The pooled keys of a ring append are made afterwards by the same pooling kernels as for plain buffers
-// (pool_part_kernel over the new ring slots, pool_finish_kernel), so they are bit-identical to pooling the written K.
+// position. The pooled keys of a ring append are made afterwards by the same pooling kernel as for plain buffers
+// (pool_mean_kernel over the new ring slots), so they are bit-identical to pooling the written K.
 #include <type_traits>
 
 #include "common.hpp"
