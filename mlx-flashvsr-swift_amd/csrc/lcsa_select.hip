@@ -131,7 +131,7 @@ __device__ __forceinline__ void wave_hist_add(unsigned* h, unsigned key, bool va
 constexpr int kScoreRows = 8;   // query blocks per workgroup (one per wave in the softmax)
 constexpr int kScoreThreads = 512;   // 8 waves: two halves of 4 stage alternate key chunks side by side
 constexpr int kKeyChunk = 64;   // key blocks staged in LDS at a time by one half
-constexpr int kChunksInFlight = 2;   // chunk loads each half keeps in flight (registers)
+constexpr int kChunksInFlight = 3;   // chunk loads each half keeps in flight (registers)
 constexpr int kKStride = kHeadDim + 4;   // padded LDS row of a pooled key (floats)
 constexpr int kHistBins = 4096; // top-12-bit bins (bits 30..19) of the prob bit patterns
 
@@ -191,15 +191,9 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
       if (jj < nj) pre[i] = *(const f32x4*)(kbase + (kmap.row(j0 + jj) / kBlock) * C + 4 * c4);
     }
   };
-  float qa[32];   // this lane's A operands (query row li, dims 32 lg .. 32 lg + 31; rows >= 8 are zero)
-#pragma unroll
-  for (int t = 0; t < 32; t += 4) {
-    const f32x4 x = li < kScoreRows ? *(const f32x4*)(qs + li * kHeadDim + 32 * lg + t) : f32x4{0.f, 0.f, 0.f, 0.f};
-    qa[t] = x[0];
-    qa[t + 1] = x[1];
-    qa[t + 2] = x[2];
-    qa[t + 3] = x[3];
-  }
+  // this lane's A operands, read from LDS at each step: query row li, dims 32 lg .. 32 lg + 31 (lanes li >= 8 read
+  // row 7 again: rows >= 8 of the product are not stored)
+  const float* qrow = qs + min(li, kScoreRows - 1) * kHeadDim + 32 * lg;
   // one round: each half stages its chunk (j0 < nk) and multiplies it; both halves take part in the barriers
   auto chunk = [&](f32x4 (&pre)[kLoads], int j0, int j_next) {
     const int nj = j0 < nk ? min(kKeyChunk, nk - j0) : 0;
@@ -217,10 +211,11 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
 #pragma unroll
       for (int t = 0; t < 32; t += 4) {
         const f32x4 kb = *(const f32x4*)(krow + t);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t], kb[0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 1], kb[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 2], kb[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[t + 3], kb[3], acc, 0, 0, 0);
+        const f32x4 qv = *(const f32x4*)(qrow + t);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[0], kb[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[1], kb[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[2], kb[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[3], kb[3], acc, 0, 0, 0);
       }
       const int jj = 16 * hw + li, j = j0 + jj;
       if (4 * lg < kScoreRows && jj < nj) {   // rows 4 lg .. 4 lg + 3 that are query rows of the group
