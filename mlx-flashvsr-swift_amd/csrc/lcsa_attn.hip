@@ -457,7 +457,20 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     for (int q = 0; q < QG; ++q)
 #pragma unroll
       for (int u = 0; u < 2; ++u) pB[q][u] = bf16x8{};
-    sync_steps(2);   // K(1), V(-1) landed
+    sync_steps(1);   // K(1), K(2), V(-1), V(0) landed
+    // the first LDS operands of a step (K chunk 0 of its QK tile, V^T pair 0 of its PV tile) are read at the end of
+    // the step before it, so no operand read sits between the step's barrier and its first MFMA; for step 0:
+    // K(1) in slot 1, V(-1) in slot 3
+    bf16x8 hk;
+    i16x4 hva, hvb;
+    auto read_first = [&](auto kslot_c, auto vslot_c) {
+      constexpr int KSL = decltype(kslot_c)::value, VSL = decltype(vslot_c)::value;
+      lds_char* const pa = lds + kVRing + VSL * kTileBytes + v_off[0];
+      hva = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
+      hvb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pa + 8 * kRowBytes));
+      hk = *(const lds_bf16x8*)(lds + KSL * kTileBytes + k_off[0]);
+    };
+    if (MODE != 1) read_first(C1{}, C3{});
 
     // step with tile T in ring slot SUB: K(T+4) -> slot SUB, V(T+2) -> slot SUB+2, QK(T+1) <- K slot SUB+1,
     // PV(T-1) <- V slot SUB+3 (all mod 4)
@@ -487,6 +500,12 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
         bf16x8 kk[8];
         // operands of QK chunk j and PV pair j: K chunk j and V^T pair j
         auto read_ops = [&](int j) {
+          if (j == 0) {   // read at the end of the step before
+            va[0] = hva;
+            vb[0] = hvb;
+            kk[0] = hk;
+            return;
+          }
           lds_char* const pa = vbase + v_off[j & 3] + 16 * (j >> 2) * kRowBytes;
           va[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)pa);
           vb[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(pa + 8 * kRowBytes));
@@ -545,6 +564,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
             xv[I & 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[q][idx], c_scale, negm[q]));
           }
           if constexpr ((I & 3) == 1 && I / 4 < kDmaStep) dma(std::integral_constant<int, I / 4>{});
+          if constexpr (I == kExt + 16 * QG - (DENSE ? 1 : 0))
+            read_first(std::integral_constant<int, (SUB + 2) & 3>{}, std::integral_constant<int, SUB>{});
           __builtin_amdgcn_sched_barrier(0);
         };
         static_for<0, kExt + 16 * QG + (DENSE ? 0 : 1)>(micro);
@@ -594,9 +615,10 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
           for (int q = 0; q < QG; ++q) mask_tile(s_nxt[q], valid_next);
         }
       }
-      // keep every instruction of this step on its side of the barrier
+      // keep every instruction of this step on its side of the barrier; the copies of the step before have landed
+      // (the next step's first operands, read above, were waited for one step earlier)
       __builtin_amdgcn_sched_barrier(0);
-      sync_steps(2);
+      sync_steps(1);
       __builtin_amdgcn_sched_barrier(0);
     };
     for (int b = 0; b < nblocks; ++b) {
