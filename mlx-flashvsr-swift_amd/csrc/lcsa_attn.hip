@@ -686,8 +686,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 }
 
 // Rows (head, query block) for the persistent bf16 walk, and the per-XCD queue counters. One workgroup. First a
-// counting sort by decreasing key-list length in bins of 8 blocks (255 bins; longer lists share the last one; the
-// dense walk: every non-empty row is a full walk). Then every wave of `grid` consecutive items of that order (one
+// counting sort by decreasing key-list length in 255 bins of ceil(longest / 255) blocks (exact lengths up to 255
+// blocks; the dense walk: every non-empty row is a full walk). Then every wave of `grid` consecutive items of that order (one
 // item per workgroup) is re-sorted by row id (head-major, neighbouring query blocks together) and dealt so that XCD x
 // (workgroups b with b % 8 == x, dispatch is round-robin over the XCDs) holds positions x, x + 8, .. of the wave:
 // one contiguous range of rows, whose key lists overlap, so the XCD's L2 serves the key blocks they share.
@@ -709,18 +709,34 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
   __shared__ int wpre[kWords];                                            // set bits in the words before word w
   __shared__ int lord[kOrderLdsRows];                                     // the sorted order (rows <= kOrderLdsRows)
   __shared__ uint8_t lbin[kOrderLdsRows];                                 // each row's bin (rows <= kOrderLdsRows)
+  __shared__ int s_longest;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool in_lds = rows <= kOrderLdsRows;
   int* const sorted = in_lds ? lord : order;
   if (tid < kBins) bin_start[tid] = 0;
+  if (tid == 0) s_longest = 0;
   __syncthreads();
-  auto bin_of = [&](int r) -> int {   // bin 0 = the longest lists
-    const int c = kcnt[r];
-    const int len = c <= 0 ? 0 : (dense ? 1 : min((min(c, nk_stride) + 7) >> 3, kBins - 1));
+  auto list_len = [&](int r) -> int { return max(0, min(kcnt[r], nk_stride)); };
+  // the longest list (the lengths wait in lord until the sort overwrites it)
+  {
+    int m = 0;
+    for (int r = tid; r < rows; r += 1024) {
+      const int c = list_len(r);
+      if (in_lds) lord[r] = c;
+      m = max(m, c);
+    }
+    for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o));
+    if (lane == 0) atomicMax(&s_longest, m);
+  }
+  __syncthreads();
+  const int width = max(1, (s_longest + kBins - 2) / (kBins - 1));   // blocks per bin
+  auto bin_len = [&](int c) -> int {   // bin 0 = the longest lists
+    const int len = c <= 0 ? 0 : (dense ? 1 : min((c + width - 1) / width, kBins - 1));
     return kBins - 1 - len;
   };
+  auto bin_of = [&](int r) -> int { return bin_len(list_len(r)); };
   for (int r = tid; r < rows; r += 1024) {
-    const int bn = bin_of(r);
+    const int bn = in_lds ? bin_len(lord[r]) : bin_of(r);
     if (in_lds) lbin[r] = (uint8_t)bn;
     atomicAdd(&bin_start[bn], 1);
   }
