@@ -36,7 +36,8 @@ int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices
                      hipStream_t stream);
 int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int C, int t0,
                         const void* wq, const void* wk, float eps, const float* rope, void* q_out, void* k_out,
-                        void* v_out, int dst_slot0, int capacity, int slice_blocks, hipStream_t stream);
+                        void* v_out, int dst_slot0, int capacity, int slice_blocks, int64_t kv_head_stride,
+                        hipStream_t stream);
 int launch_pool_mean(int dtype, PoolMean* jobs, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream);
 int launch_pool_finish(const PoolDst* dst, int n, int C, unsigned* zero, int64_t nzero, hipStream_t stream);
 int rope_table_floats();
@@ -53,10 +54,10 @@ int noalloc_scratch_init(int device);
 int noalloc_scratch(int device, int64_t rows, int32_t** order, int32_t** counter);
 void rope_tables_host(double theta, float* out);
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
-                       int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
-                       float* partial, hipStream_t stream);
+                       int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, int64_t head_stride,
+                       float* pooled, float* partial, hipStream_t stream);
 int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,
-                     KeyMap map, hipStream_t stream);
+                     int64_t head_stride, KeyMap map, hipStream_t stream);
 int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int w, int C, bool to_windows,
                          hipStream_t stream);
 
@@ -107,7 +108,9 @@ struct fvsr_kv_ring {
   fvsr_ctx* ctx = nullptr;
   int dtype = 0, layers = 0, heads = 0, bh = 0, bw = 0, s = 0, capacity = 0, kv_len = 0, C = 0;
   std::vector<int> head, count;
-  void* k = nullptr;         // (layers, capacity * s * 128, C)
+  // (layers, heads, capacity * s * 128, 128): head-major per layer, so a 32-key tile of one head is one contiguous
+  // 8 KB run (bf16) rather than 32 rows 3 KB apart
+  void* k = nullptr;
   void* v = nullptr;
   float* pooled = nullptr;   // (layers, capacity * s, C)
   float* partial = nullptr;  // (capacity * s * kPoolParts, C): pooled-key runs of one append
@@ -116,6 +119,7 @@ struct fvsr_kv_ring {
   char* layer_v(int l) const { return (char*)v + (size_t)l * layer_tokens() * C * esize(dtype); }
   float* layer_pooled(int l) const { return pooled + (size_t)l * capacity * s * C; }
   KeyMap map(int l) const { return make_key_map(head[l], capacity, s); }
+  int64_t head_stride() const { return (int64_t)layer_tokens() * kHeadDim; }   // elements between heads of a layer
 };
 
 #define FVSR_REQUIRE(cond, status, msg) \
@@ -258,8 +262,8 @@ static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, con
     // block means of Q (and K) and the histogram reset, one launch
     PoolMean jobs[2];
     int n = 0;
-    if (!q_pooled) jobs[n++] = PoolMean{qW, lq, pq, 0, 0, 1, 1 << 30};
-    if (!pk_ready) jobs[n++] = PoolMean{kW, lk, (float*)(ws + cv.pk), 0, 0, 1, 1 << 30};
+    if (!q_pooled) jobs[n++] = PoolMean{qW, lq, pq, 0, 0, 1, 1 << 30, 0};
+    if (!pk_ready) jobs[n++] = PoolMean{kW, lk, (float*)(ws + cv.pk), 0, 0, 1, 1 << 30, 0};
     if ((rc = launch_pool_mean(dtype, jobs, n, C, q_pooled ? nullptr : hist,
                                (int64_t)(hist12_bytes(heads, q_slices) / sizeof(unsigned)), stream)))
       return rc;
@@ -290,9 +294,10 @@ int fvsr_lcsa_select(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const
 // ---------------------------------------------------------------------------------------------------------------
 // attention
 // ---------------------------------------------------------------------------------------------------------------
+// K/V token-major (rows of heads * 128 elements of es bytes, lk rows); the ring's head-major layout is set by its caller
 static AttnArgs make_args(const void* q, int64_t lq, const void* k, const void* v, int64_t lk, int heads,
                           const int32_t* kidx, const int32_t* kcnt, const uint8_t* sel, int nk_stride, int nk,
-                          KeyMap map, void* o) {
+                          KeyMap map, void* o, int es) {
   AttnArgs a{};
   a.q = q; a.k = k; a.v = v; a.o = o;
   a.lq = lq; a.lk = lk;
@@ -302,7 +307,9 @@ static AttnArgs make_args(const void* q, int64_t lq, const void* k, const void* 
   a.nq = (int)ceil_div(lq, kBlock);
   a.nk = nk;
   a.map = map;
-  a.kv_rows = lk;
+  a.kv_head_stride = kHeadDim;
+  a.kv_ld = a.ld;
+  a.kv_bytes = lk * a.ld * es;
   a.c = (float)(1.4426950408889634 / std::sqrt((double)kHeadDim));
   return a;
 }
@@ -341,7 +348,7 @@ int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, con
   FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
   const int nk = (int)ceil_div(lk, kBlock);
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
-  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o, esize(dtype));
   if ((rc = attach_order(ctx, a, nk))) return rc;
   return launch_attention(dtype, false, a, (hipStream_t)stream);
 }
@@ -354,7 +361,7 @@ int fvsr_lcsa_attention_noalloc(fvsr_ctx* ctx, int dtype, const void* q, int64_t
   FVSR_REQUIRE(kidx && kcnt, FVSR_ERR_INVALID_ARG, "kidx and kcnt must be non-NULL");
   FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
   const int nk = (int)ceil_div(lk, kBlock);
-  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o, esize(dtype));
   if ((rc = noalloc_scratch(ctx->device, (int64_t)heads * a.nq, &a.order, &a.counter))) return rc;
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   return launch_attention(dtype, false, a, (hipStream_t)stream);
@@ -377,7 +384,7 @@ int fvsr_lcsa_attention_mask(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq
   hipStream_t st = (hipStream_t)stream;
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   if ((rc = launch_lists_from_mask(block_mask, (int)(heads * nq), (int)nk, kidx, kcnt, sel, st))) return rc;
-  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, plain_key_map(), o);
+  AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, sel, (int)nk, (int)nk, plain_key_map(), o, esize(dtype));
   if ((rc = attach_order(ctx, a, nk))) return rc;
   return launch_attention(dtype, mode == FVSR_ATTN_DENSE, a, st);
 }
@@ -444,7 +451,7 @@ int fvsr_qkv_epilogue(fvsr_ctx* ctx, int dtype, const void* q, const void* k, co
   FVSR_REQUIRE(q_out && k_out && v_out, FVSR_ERR_INVALID_ARG, "q_out, k_out and v_out must be non-NULL");
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   return launch_qkv_epilogue(dtype, q, k, v, f, h, w, heads * 128, t0, norm_q_weight, norm_k_weight, eps,
-                             rope_tables, q_out, k_out, v_out, 0, 1, 1 << 30, (hipStream_t)stream);
+                             rope_tables, q_out, k_out, v_out, 0, 1, 1 << 30, 0, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -538,8 +545,8 @@ int fvsr_kv_ring_append(fvsr_kv_ring* r, int layer, const void* k_new, const voi
   FVSR_HIP_CHECK(hipSetDevice(r->ctx->device));
   const int slot0 = (r->head[layer] + r->count[layer]) % r->capacity;
   rc = launch_ring_append(r->dtype, k_new, v_new, n_slices * r->s, r->C, layout == FVSR_LAYOUT_GRID, r->bh, r->bw,
-                          slot0, r->capacity, r->layer_k(layer), r->layer_v(layer), r->layer_pooled(layer),
-                          r->partial, (hipStream_t)stream);
+                          slot0, r->capacity, r->layer_k(layer), r->layer_v(layer), r->head_stride(),
+                          r->layer_pooled(layer), r->partial, (hipStream_t)stream);
   if (rc) return rc;
   r->count[layer] += n_slices;
   return FVSR_OK;
@@ -569,21 +576,22 @@ static int append_qkv_impl(fvsr_kv_ring* r, int layer, const void* q, const void
   const int nb = n_slices * r->s;
   rc = launch_qkv_epilogue(r->dtype, q, k, v, 2 * n_slices, 8 * r->bh, 8 * r->bw, r->C, t0, norm_q_weight,
                            norm_k_weight, eps, rope_tables, q_out, r->layer_k(layer), r->layer_v(layer), slot0,
-                           r->capacity, r->s, stream);
+                           r->capacity, r->s, r->head_stride(), stream);
   if (rc) return rc;
   // pooled keys of the new slots, as for plain buffers: block means over the slots up to the end of the ring, then
-  // the wrapped remainder from slot 0 (and the queries' means, and the histogram reset), one launch
+  // the wrapped remainder from slot 0 (and the queries' means, and the histogram reset), one launch; a slot's first
+  // token in head 0's region of the (head-major) ring is s * 128 rows of 128 elements past the previous slot's
   const int first = std::min(n_slices, r->capacity - slot0);
-  const size_t slot_bytes = (size_t)r->s * kBlock * r->C * esize(r->dtype);
+  const size_t slot_bytes = (size_t)r->s * kBlock * kHeadDim * esize(r->dtype);
   const int64_t lq = (int64_t)nb * kBlock;
   PoolMean jobs[3];
   int nj = 0;
   jobs[nj++] = PoolMean{r->layer_k(layer) + slot0 * slot_bytes, (int64_t)first * r->s * kBlock,
-                        r->layer_pooled(layer), 0, slot0, r->capacity, r->s};
+                        r->layer_pooled(layer), 0, slot0, r->capacity, r->s, r->head_stride()};
   if (first < n_slices)
     jobs[nj++] = PoolMean{r->layer_k(layer), (int64_t)(n_slices - first) * r->s * kBlock, r->layer_pooled(layer), 0,
-                          0, r->capacity, r->s};
-  if (q_pooled) jobs[nj++] = PoolMean{q_out, lq, q_pooled, 0, 0, 1, 1 << 30};
+                          0, r->capacity, r->s, r->head_stride()};
+  if (q_pooled) jobs[nj++] = PoolMean{q_out, lq, q_pooled, 0, 0, 1, 1 << 30, 0};
   if ((rc = launch_pool_mean(r->dtype, jobs, nj, r->C, hist, nhist, stream))) return rc;
   r->count[layer] += n_slices;
   return FVSR_OK;
@@ -623,7 +631,7 @@ int fvsr_kv_ring_read(fvsr_kv_ring* r, int layer, void* k_out, void* v_out, void
   FVSR_REQUIRE(k_out && v_out, FVSR_ERR_INVALID_ARG, "k_out and v_out must be non-NULL");
   FVSR_HIP_CHECK(hipSetDevice(r->ctx->device));
   return launch_ring_read(r->dtype, r->layer_k(layer), r->layer_v(layer), k_out, v_out, r->count[layer] * r->s,
-                          r->C, r->map(layer), (hipStream_t)stream);
+                          r->C, r->head_stride(), r->map(layer), (hipStream_t)stream);
 }
 
 int fvsr_lcsa_select_ring(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const void* qW, int64_t lq, int q_slices,
@@ -647,8 +655,10 @@ static int attention_ring_impl(fvsr_ctx* ctx, fvsr_kv_ring* r, int layer, const 
                                bool dense, void* o, hipStream_t stream, bool o_grid = false) {
   const int nk = r->count[layer] * r->s;
   AttnArgs a = make_args(q, lq, r->layer_k(layer), r->layer_v(layer), (int64_t)nk * kBlock, r->heads, kidx, kcnt,
-                         sel, nk_stride, nk, r->map(layer), o);
-  a.kv_rows = (int64_t)r->layer_tokens();
+                         sel, nk_stride, nk, r->map(layer), o, esize(r->dtype));
+  a.kv_head_stride = r->head_stride();   // head-major
+  a.kv_ld = kHeadDim;
+  a.kv_bytes = (int64_t)r->heads * r->head_stride() * esize(r->dtype);
   if (o_grid) {   // whole windows of the ring's (8 bh, 8 bw) grid: write o in natural token order
     a.o_nbh = r->bh;
     a.o_nbw = r->bw;

@@ -94,13 +94,21 @@ inline KeyMap plain_key_map() { return make_key_map(0, 1, 1 << 16); }
 
 // One job of pool_mean_kernel (lcsa_select.hip): the block means of the L tokens of x (nb = ceil(L / 128) blocks);
 // block b is written to row ((slot0 + b / slice_blocks) % capacity) * slice_blocks + b % slice_blocks of out (a ring
-// slot mapping; slot0 0, capacity 1, slice_blocks >= nb for a plain buffer).
+// slot mapping; slot0 0, capacity 1, slice_blocks >= nb for a plain buffer). x is token-major (rows of C channels)
+// when head_stride is 0, else head-major: channel c of token t at (c / 128) * head_stride + t * 128 + c % 128.
 struct PoolMean {
   const void* x;
   int64_t L;
   float* out;
   int nb, slot0, capacity, slice_blocks;
+  int64_t head_stride;
 };
+
+// element offset of (token t, channel c) in a buffer of C channels per token: token-major when head_stride is 0,
+// else head-major (each head's 128 channels of all tokens contiguous, head h at h * head_stride)
+__host__ __device__ __forceinline__ int64_t kv_offset(int64_t t, int c, int C, int64_t head_stride) {
+  return head_stride == 0 ? t * C + c : (int64_t)(c / kHeadDim) * head_stride + t * kHeadDim + c % kHeadDim;
+}
 
 // One block-mean target of pool_finish_kernel (kv_ring.hip): nb blocks (L tokens) of run sums in partial; block b
 // is written to row ((slot0 + b / slice_blocks) % capacity) * slice_blocks + b % slice_blocks of out (a ring
@@ -129,7 +137,10 @@ struct AttnArgs {
   int nq;
   int nk;
   KeyMap map;
-  int64_t kv_rows;       // token rows physically present in the k/v buffers (buffer-load range)
+  int64_t kv_head_stride;   // elements from head h's K/V to head h + 1's: 128 in token-major buffers (rows of
+                            // heads * 128), rows * 128 in head-major ones (each head's rows contiguous: the KV ring)
+  int kv_ld;                // elements between consecutive K/V token rows: heads * 128 or 128
+  int64_t kv_bytes;         // bytes of each of the k and v buffers (the buffer-load range), < 2 GiB
   float c;               // softmax scale * log2(e)
   int32_t* order;        // (H * nq) rows, longest key list first (bf16 persistent walk; workspace)
   int32_t* counter;      // per-XCD queue counters of the walk, counter[8 x] for XCD x (workspace, 256 bytes; set by

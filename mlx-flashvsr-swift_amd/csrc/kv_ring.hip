@@ -21,7 +21,8 @@ namespace fvsr {
 template <typename T>
 __global__ void block_copy_kernel(const T* __restrict__ src, T* __restrict__ dst, int C, bool src_grid,
                                   bool dst_grid, int nbh, int nbw, int dst_slot0, int capacity, int slice_blocks,
-                                  float* __restrict__ partial, const T* __restrict__ src2, T* __restrict__ dst2) {
+                                  float* __restrict__ partial, const T* __restrict__ src2, T* __restrict__ dst2,
+                                  int64_t dst_head_stride) {
   constexpr int VN = 16 / sizeof(T);
   constexpr int kRun = kBlock / kPoolParts;
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -38,9 +39,10 @@ __global__ void block_copy_kernel(const T* __restrict__ src, T* __restrict__ dst
     for (int t = part * kRun; t < (part + 1) * kRun; ++t) {
       const int64_t si = src_grid ? window_token_to_grid(b, t, nbh, nbw) : (int64_t)b * kBlock + t;
       const int64_t di = dst_grid ? window_token_to_grid((int)db, t, nbh, nbw) : db * kBlock + t;
+      const int64_t dof = kv_offset(di, cv * VN, C, dst_head_stride);   // token-major, or head-major (a ring)
       const u4 x = *(const u4*)(src + si * C + cv * VN);
-      *(u4*)(dst + di * C + cv * VN) = x;
-      if (src2) *(u4*)(dst2 + di * C + cv * VN) = *(const u4*)(src2 + si * C + cv * VN);
+      *(u4*)(dst + dof) = x;
+      if (src2) *(u4*)(dst2 + dof) = *(const u4*)(src2 + si * C + cv * VN);
       if (partial) {
         const T* xv = (const T*)&x;
 #pragma unroll
@@ -93,7 +95,7 @@ int launch_pool_finish(const PoolDst* dst, int n, int C, unsigned* zero, int64_t
 // Ring -> window order: logical block j of the held window (slot (head + j/s) % capacity) -> block j of dst.
 template <typename T>
 __global__ void ring_read_kernel(const T* __restrict__ rk, const T* __restrict__ rv, T* __restrict__ ok,
-                                 T* __restrict__ ov, int C, KeyMap map) {
+                                 T* __restrict__ ov, int C, int64_t head_stride, KeyMap map) {
   constexpr int VN = 16 / sizeof(T);
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
   const int j = blockIdx.x;
@@ -101,8 +103,9 @@ __global__ void ring_read_kernel(const T* __restrict__ rk, const T* __restrict__
   const int nvec = C / VN;
   for (int e = threadIdx.x; e < kBlock * nvec; e += blockDim.x) {
     const int t = e / nvec, cv = e % nvec;
-    *(u4*)(ok + (dr + t) * C + cv * VN) = *(const u4*)(rk + (sr + t) * C + cv * VN);
-    *(u4*)(ov + (dr + t) * C + cv * VN) = *(const u4*)(rv + (sr + t) * C + cv * VN);
+    const int64_t so = kv_offset(sr + t, cv * VN, C, head_stride);
+    *(u4*)(ok + (dr + t) * C + cv * VN) = *(const u4*)(rk + so);
+    *(u4*)(ov + (dr + t) * C + cv * VN) = *(const u4*)(rv + so);
   }
 }
 
@@ -113,19 +116,19 @@ static int copy_threads(int C, int esize) {
 
 // partial: (n_blocks * kPoolParts, C) fp32 scratch for the pooled-key runs
 int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_blocks, int C, bool grid_layout,
-                       int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, float* pooled,
-                       float* partial, hipStream_t stream) {
+                       int nbh, int nbw, int slot0, int capacity, void* ring_k, void* ring_v, int64_t head_stride,
+                       float* pooled, float* partial, hipStream_t stream) {
   if (n_blocks <= 0) return FVSR_OK;
   const int s = nbh * nbw;
   const dim3 grid(n_blocks, kPoolParts);
   if (dtype == FVSR_DTYPE_BF16) {
     hipLaunchKernelGGL(block_copy_kernel<bf16>, grid, dim3(copy_threads(C, 2)), 0, stream, (const bf16*)k_new,
                        (bf16*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s, partial,
-                       (const bf16*)v_new, (bf16*)ring_v);
+                       (const bf16*)v_new, (bf16*)ring_v, head_stride);
   } else {
     hipLaunchKernelGGL(block_copy_kernel<float>, grid, dim3(copy_threads(C, 4)), 0, stream, (const float*)k_new,
                        (float*)ring_k, C, grid_layout, false, nbh, nbw, slot0, capacity, s, partial,
-                       (const float*)v_new, (float*)ring_v);
+                       (const float*)v_new, (float*)ring_v, head_stride);
   }
   FVSR_HIP_CHECK(hipGetLastError());
   const PoolDst d{partial, pooled, (int64_t)n_blocks * kBlock, n_blocks, slot0, capacity, s};
@@ -133,14 +136,14 @@ int launch_ring_append(int dtype, const void* k_new, const void* v_new, int n_bl
 }
 
 int launch_ring_read(int dtype, const void* rk, const void* rv, void* ok, void* ov, int n_blocks, int C,
-                     KeyMap map, hipStream_t stream) {
+                     int64_t head_stride, KeyMap map, hipStream_t stream) {
   if (n_blocks <= 0) return FVSR_OK;
   if (dtype == FVSR_DTYPE_BF16)
     hipLaunchKernelGGL(ring_read_kernel<bf16>, dim3(n_blocks), dim3(256), 0, stream, (const bf16*)rk,
-                       (const bf16*)rv, (bf16*)ok, (bf16*)ov, C, map);
+                       (const bf16*)rv, (bf16*)ok, (bf16*)ov, C, head_stride, map);
   else
     hipLaunchKernelGGL(ring_read_kernel<float>, dim3(n_blocks), dim3(256), 0, stream, (const float*)rk,
-                       (const float*)rv, (float*)ok, (float*)ov, C, map);
+                       (const float*)rv, (float*)ok, (float*)ov, C, head_stride, map);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }
@@ -155,11 +158,11 @@ int launch_window_layout(int dtype, const void* x, void* out, int f, int h, int 
   if (dtype == FVSR_DTYPE_BF16)
     hipLaunchKernelGGL(block_copy_kernel<bf16>, dim3(n_blocks, kPoolParts), dim3(copy_threads(C, 2)), 0, stream,
                        (const bf16*)x, (bf16*)out, C, to_windows, !to_windows, nbh, nbw, 0, 1, big,
-                       (float*)nullptr, (const bf16*)nullptr, (bf16*)nullptr);
+                       (float*)nullptr, (const bf16*)nullptr, (bf16*)nullptr, (int64_t)0);
   else
     hipLaunchKernelGGL(block_copy_kernel<float>, dim3(n_blocks, kPoolParts), dim3(copy_threads(C, 4)), 0, stream,
                        (const float*)x, (float*)out, C, to_windows, !to_windows, nbh, nbw, 0, 1, big,
-                       (float*)nullptr, (const float*)nullptr, (float*)nullptr);
+                       (float*)nullptr, (const float*)nullptr, (float*)nullptr, (int64_t)0);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }

@@ -235,17 +235,20 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
   }
 
   // tile loads: the buffer spans the physical K/V rows; a row past it reads as 0, so a ragged last block, a listed
-  // index outside [0, nk) and the tiles past the end of the walk load zeros without per-lane guards
-  const uint32_t row_bytes = (uint32_t)a.ld * 2;
-  const uint32_t range = (uint32_t)(a.kv_rows * row_bytes);
+  // index outside [0, nk) and the tiles past the end of the walk load zeros without per-lane guards. K/V rows are
+  // token-major (head h's 128 channels at 256 h bytes of each row) or head-major (a KV ring: head h's rows from
+  // h * kv_head_stride on, 256 bytes each; every block whole, so no row past a head's region is read)
+  const uint32_t row_bytes = (uint32_t)a.kv_ld * 2;
+  const uint32_t range = (uint32_t)a.kv_bytes;
+  const int head_off = (int)(h * a.kv_head_stride * 2);
   const u32x4 krs = buffer_rsrc(a.k, range), vrs = buffer_rsrc(a.v, range);
   // a DMA load writes 1 KB of LDS (lane i -> bytes 16i..16i+15) = 4 rows; wave w fills rows kWaveRows * w ..
   int voff_k[kDmaK], voff_v[kDmaK];
 #pragma unroll
   for (int p = 0; p < kDmaK; ++p) {
     const int r = wave * kWaveRows + 4 * p + (lane >> 4), pos = lane & 15;
-    voff_k[p] = r * (int)row_bytes + hc * 2 + ((pos ^ swz_k(r)) << 4);
-    voff_v[p] = r * (int)row_bytes + hc * 2 + ((pos ^ swz_v(r)) << 4);
+    voff_k[p] = r * (int)row_bytes + head_off + ((pos ^ swz_k(r)) << 4);
+    voff_v[p] = r * (int)row_bytes + head_off + ((pos ^ swz_v(r)) << 4);
   }
   const uint32_t smem_lds = lds_addr(smem);
   const uint32_t dma_base = smem_lds + wave * kWaveRows * kRowBytes;
@@ -900,7 +903,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnArgs a) {
     for (int p = 0; p < 4; ++p) {
       const int r = p * 8 + ld_row;
       if (r < valid) {
-        const int64_t off = (row0 + r) * a.ld + hc + ld_c4 * 4;
+        const int64_t off = (row0 + r) * a.kv_ld + h * a.kv_head_stride + ld_c4 * 4;
         kreg[p] = *(const f32x4*)(K + off);
         vreg[p] = *(const f32x4*)(V + off);
       } else {

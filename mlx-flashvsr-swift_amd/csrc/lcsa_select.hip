@@ -79,14 +79,15 @@ __global__ __launch_bounds__(kPoolParts * kPoolVecs) void pool_mean_kernel(PoolM
   const T* __restrict__ x = (const T*)job.x;
   const int64_t r0 = (int64_t)b * kBlock + part * kRun;
   const int n = (int)max<int64_t>(0, min<int64_t>(kRun, job.L - r0));
+  const int64_t rstride = job.head_stride == 0 ? C : kHeadDim;   // elements between token rows
   float acc[VN];
 #pragma unroll
   for (int e = 0; e < VN; ++e) acc[e] = 0.f;
   if (cv < nvec) {
-    const T* p = x + r0 * C + cv * VN;
+    const T* p = x + kv_offset(r0, cv * VN, C, job.head_stride);
 #pragma unroll 8
     for (int r = 0; r < n; ++r) {
-      const VT v = *(const VT*)(p + (int64_t)r * C);
+      const VT v = *(const VT*)(p + (int64_t)r * rstride);
 #pragma unroll
       for (int e = 0; e < VN; ++e) acc[e] += (float)v[e];
     }

@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int64_t L, int C, int nbh, int nbw,
     int t0, const T* __restrict__ wq, const T* __restrict__ wk, float eps, const float* __restrict__ rope,
     T* __restrict__ q_out, T* __restrict__ k_out, T* __restrict__ v_out, int dst_slot0, int capacity,
-    int slice_blocks) {
+    int slice_blocks, int64_t kv_head_stride) {
   constexpr int VN = 16 / sizeof(T);
   constexpr int kMaxVec = NV;
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -130,14 +130,16 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(
       rk[2 * p + 1] = (T)__fadd_rn(__fmul_rn(kre, sn), __fmul_rn(kim, cs));
     }
     *(u4*)(q_out + ((int64_t)b * kBlock + t) * C + c0) = oq;
-    *(u4*)(k_out + (db * kBlock + t) * C + c0) = ok;
-    *(u4*)(v_out + (db * kBlock + t) * C + c0) = xv[j];
+    const int64_t kvo = kv_offset(db * kBlock + t, c0, C, kv_head_stride);   // token-major, or head-major (a ring)
+    *(u4*)(k_out + kvo) = ok;
+    *(u4*)(v_out + kvo) = xv[j];
   }
 }
 
 int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int C, int t0,
                         const void* wq, const void* wk, float eps, const float* rope, void* q_out, void* k_out,
-                        void* v_out, int dst_slot0, int capacity, int slice_blocks, hipStream_t stream) {
+                        void* v_out, int dst_slot0, int capacity, int slice_blocks, int64_t kv_head_stride,
+                        hipStream_t stream) {
   const int nbh = h / 8, nbw = w / 8;
   const int64_t L = (int64_t)f * h * w;
   if (L <= 0) return FVSR_OK;
@@ -150,11 +152,13 @@ int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, 
     if (dtype == FVSR_DTYPE_BF16)
       hipLaunchKernelGGL((qkv_epilogue_kernel<bf16, NV>), grid, dim3(256), 0, stream, (const bf16*)q,
                          (const bf16*)k, (const bf16*)v, L, C, nbh, nbw, t0, (const bf16*)wq, (const bf16*)wk, eps,
-                         rope, (bf16*)q_out, (bf16*)k_out, (bf16*)v_out, dst_slot0, capacity, slice_blocks);
+                         rope, (bf16*)q_out, (bf16*)k_out, (bf16*)v_out, dst_slot0, capacity, slice_blocks,
+                         kv_head_stride);
     else
       hipLaunchKernelGGL((qkv_epilogue_kernel<float, NV>), grid, dim3(256), 0, stream, (const float*)q,
                          (const float*)k, (const float*)v, L, C, nbh, nbw, t0, (const float*)wq, (const float*)wk,
-                         eps, rope, (float*)q_out, (float*)k_out, (float*)v_out, dst_slot0, capacity, slice_blocks);
+                         eps, rope, (float*)q_out, (float*)k_out, (float*)v_out, dst_slot0, capacity, slice_blocks,
+                         kv_head_stride);
   };
   switch (nv) {
     case 1: go(std::integral_constant<int, 1>{}); break;
