@@ -30,11 +30,17 @@ PEAK_BF16_TFLOPS = 2500.0            # MI355X dense bf16 MFMA
 PROFILE_PMC = os.path.join(ROOT, "profiles", "lcsa_attn_bf16_1920x1152_pmc.txt")
 
 
+def warmup_of(args, default):
+    return default if args.warmup is None else args.warmup
+
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default: 300 layer calls, ~0.2 s, so the part's clock has settled "
+                         "before timing; 20 for the other modes, whose warm-up already runs that long)")
     ap.add_argument("--workload", default="sparse_1920x1152_bf16")
     ap.add_argument("--seed", type=int, default=None, help="generator seed (default: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
@@ -252,7 +258,7 @@ def stream_bench(args):
             if events is not None:
                 events[c][1].record()
 
-    for _ in range(max(1, args.warmup // 5)):
+    for _ in range(max(1, warmup_of(args, 20) // 5)):
         run_stream()
     torch.cuda.synchronize()
     reps = max(1, args.steps // 10)
@@ -318,7 +324,7 @@ def epilogue_bench(args):
         if ring.slices(0) >= 3:
             ring.reset()
 
-    for _ in range(max(3, args.warmup)):
+    for _ in range(max(3, warmup_of(args, 20))):
         once()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -453,7 +459,7 @@ def block_bench(args):
     L = 2 * lat_h * lat_w
     x = rnd(L, C)
     t0 = 6
-    for _ in range(max(2, args.warmup)):
+    for _ in range(max(2, warmup_of(args, 20))):
         blk.forward(ring, 0, x, t_mod, 1, t0, local, topk)
     torch.cuda.synchronize()
     n = max(5, args.steps)
@@ -537,7 +543,7 @@ def main():
     empty_rows = int((kcnt == 0).sum().item())
     del probs
 
-    for _ in range(args.warmup):
+    for _ in range(warmup_of(args, 300)):
         _, _, ki, kc = select()
         attend(ki, kc)
     torch.cuda.synchronize()
@@ -614,7 +620,7 @@ def main():
         "unit": "TFLOP/s (effective, kept blocks; whole layer call = selection + attention)",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warmup_of(args, 300),
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
