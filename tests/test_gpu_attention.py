@@ -325,3 +325,50 @@ def test_reference_raise_on_sharp_scores(dev, density):
     rel = _rel(o, ref)
     print(f"  density {density}: rel {rel:.2e}", flush=True)
     assert rel <= BF16_REL
+
+
+_QG2_CHILD = r"""
+import sys, numpy as np, torch
+sys.path[:0] = sys.argv[3:5]
+import fvsr_lcsa
+z = np.load(sys.argv[1])
+dev = torch.device("cuda:0")
+q, k, v = (torch.from_numpy(z[n]).to(dev).to(torch.bfloat16) for n in ("q", "k", "v"))
+m = torch.from_numpy(z["mask"]).to(dev)
+heads = int(z["heads"])
+o = fvsr_lcsa.kernel_block_attention(q, k, v, m, heads)
+od = fvsr_lcsa.block_masked_attention(q, k, v, m, heads)
+torch.cuda.synchronize()
+np.savez(sys.argv[2], o=o.float().cpu().numpy(), od=od.float().cpu().numpy())
+"""
+
+
+def test_64_query_waves_equal_32_query_waves(dev, tmp_path):
+    """The bf16 walk's 64-queries-per-wave lane (FVSR_ATTN_QG=2, one wave per SIMD; read once per process, so it runs
+    in a child) does the same arithmetic per 32-query group as the default lane: kernel and dense walk bit-identical
+    to the default's, on ragged rows with an empty one and listed blocks of every length."""
+    import subprocess
+    import sys
+    heads, lqb, nkb = 4, 20, 60
+    gen = torch.Generator().manual_seed(2024)
+    q = torch.randn((lqb * 128 - 37, heads * 128), generator=gen).to(torch.bfloat16)
+    k = torch.randn((nkb * 128 - 90, heads * 128), generator=gen).to(torch.bfloat16)
+    v = torch.randn((nkb * 128 - 90, heads * 128), generator=gen).to(torch.bfloat16)
+    m = (torch.rand((heads, lqb, nkb), generator=gen) < torch.linspace(0.05, 0.9, lqb).view(1, lqb, 1)).float()
+    m[1, 3] = 0.0                              # an empty row
+    inp = tmp_path / "in.npz"
+    out = tmp_path / "out.npz"
+    np.savez(inp, q=q.float().numpy(), k=k.float().numpy(), v=v.float().numpy(), mask=m.numpy(), heads=heads)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, FVSR_ATTN_QG="2")
+    r = subprocess.run([sys.executable, "-c", _QG2_CHILD, str(inp), str(out), os.path.join(root, "mlx-flashvsr-swift_amd"),
+                        root], env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    qd, kd, vd, md = q.to(dev), k.to(dev), v.to(dev), m.to(dev)
+    o = fvsr_lcsa.kernel_block_attention(qd, kd, vd, md, heads)
+    od = fvsr_lcsa.block_masked_attention(qd, kd, vd, md, heads)
+    torch.cuda.synchronize()
+    z = np.load(out)
+    assert np.array_equal(z["o"], _np(o))
+    assert np.array_equal(z["od"], _np(od))
+    assert torch.equal(o, od)
