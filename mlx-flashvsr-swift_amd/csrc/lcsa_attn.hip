@@ -75,11 +75,12 @@ __device__ __forceinline__ float rescale_if_grown(float mxc, float& m_run, float
 // Keys stream in tiles of 32 (a quarter of a 128-key block). K and V tiles land in two LDS rings of kSlots slots by
 // buffer_load ... lds (16 B per lane, no VGPR staging); a tile's rows are 256 B (one head) with the 16-byte chunks
 // XOR-swizzled by row so the ds_read_b128 (K) and ds_read_b64_tr_b16 (V^T) operand reads are bank-conflict free.
-// While tile T is processed (step T), K of tile T+4 and V of tile T+2 are requested; they are waited for two steps
-// later, before the step that reads them.
+// While tile T is processed (step T), K of tile T+4 and V of tile T+2 are requested; each step ends by waiting for
+// the copies of the step before it, so a tile is in LDS a step before the step that first reads it.
 //
-// Softmax with a lazily raised reference per query row: S = K Q^T in fp32 from the bf16 inputs (one extra rank-1
-// MFMA per tile adds -2^100 for keys that do not take part: ragged end, unselected block of the dense walk), then
+// Softmax with a lazily raised reference per query row: S = K Q^T in fp32 from the bf16 inputs (keys that do not
+// take part score -2^100: in the dense walk by one extra rank-1 MFMA per tile, in the sparse walk by a select on the
+// rare tile with fewer than 32 keys: a ragged end, an index outside [0, nk), the tile past the walk's end), then
 // P = exp2(c S - m) with one v_fma per score (c = log2(e)/sqrt(128), applied to the fp32 scores as the reference
 // does, SparseAttention.swift:96; m, the row's reference, first the exact max of its first tile). A tile whose
 // partial row sum exceeds 2^32 (its scores outgrew the reference by about 27 or more, in log2 units) raises the
