@@ -8,8 +8,8 @@
 //   per (head, query temporal slice) keep the entries STRICTLY above the (k+1)-th largest of the s*Nk probs,
 //   k = min(n - 1, topk).
 //
-// Kernels (all HBM/L2-bound, no MFMA — the score product is 0.1 GFLOP):
-//   pool_mean_kernel     one workgroup per 128-token block (and run of up to 256 channel vectors): its four
+// Kernels (HBM- or latency-bound; the score product, 0.1 GFLOP, runs on the fp32 matrix cores):
+//   pool_mean_kernel     one workgroup per 128-token block and run of 64 channel vectors: its four
 //                        quarters sum one run of 32 tokens each (coalesced 16-byte loads, fp32), the runs meet in
 //                        LDS and the block mean ((r0 + r1) + (r2 + r3)) / n is stored (Q and K, or Q and the new
 //                        ring keys, in one launch); the launch also clears the histogram below
@@ -17,11 +17,11 @@
 //                         coalesced chunks of 64 keys, two chunks side by side, read once per 8 query rows; scores
 //                         + local mask in LDS, one wave per row for max / exp / sum / normalise; it also counts the
 //                         nonzero probs of each (head, query slice) per top-12-bit bin
-//   topk_threshold_kernel one 1024-thread workgroup per (head, query slice): exact (k+1)-th largest over the fp32
-//                         bit patterns (probs are >= 0, so bit order = value order): the row is loaded into
-//                         registers at once, the histogram picks the bin, its elements are gathered to LDS and
-//                         three radix passes finish the low 19 bits (full-row 4-pass radix select when the bin is
-//                         too large)
+//   topk_threshold_kernel 16 workgroups of 256 threads per (head, query slice): exact (k+1)-th largest over the
+//                         fp32 bit patterns (probs are >= 0, so bit order = value order): the histogram picks the
+//                         bin, each workgroup gathers the bin's elements of its share of the row (held in
+//                         registers), and the last to arrive finishes the low 19 bits by three radix passes in LDS
+//                         (full-row 4-pass radix select when the bin is too large)
 //   topk_emit_kernel     one wave per query row: mask, selection bytes and compacted key lists (ballot + popcount)
 #include "common.hpp"
 
@@ -48,7 +48,8 @@ struct Vec16<bf16> {
 // rows [b*128 + 32*part, +32) that exist, in row order, for channel vectors y*per .. y*per + per - 1; the mean is
 // ((r0 + r1) + (r2 + r3)) / n, the order the ring append's runs are finished in (pool_finish_kernel), so pooled keys
 // are bit-identical whichever path wrote them. Every workgroup also clears its share of `zero` (nzero words).
-constexpr int kPoolVecs = 256;   // channel vectors per workgroup quarter, at most
+constexpr int kPoolVecs = 64;   // channel vectors per workgroup quarter: a 1536-channel block takes 3 workgroups, so
+                                // even a one-slice append (135 blocks) spreads over every CU
 template <typename T>
 __global__ __launch_bounds__(kPoolParts * kPoolVecs) void pool_mean_kernel(PoolMean j0, PoolMean j1, PoolMean j2,
                                                                           int C, unsigned* __restrict__ zero,
@@ -597,7 +598,7 @@ int launch_pool_mean(int dtype, PoolMean* jobs, int n, int C, unsigned* zero, in
   if (nb <= 0 && nzero <= 0) return FVSR_OK;
   const int vn = dtype == FVSR_DTYPE_BF16 ? 8 : 4;
   const int nvec = C / vn;
-  const int per = std::min(kPoolVecs, ((nvec + 63) / 64) * 64);   // threads per quarter
+  const int per = kPoolVecs;   // threads per quarter
   const dim3 grid(std::max(nb, 1), (unsigned)ceil_div(nvec, per));
   if (dtype == FVSR_DTYPE_BF16)
     hipLaunchKernelGGL(pool_mean_kernel<bf16>, grid, dim3(kPoolParts * per), 0, stream, j[0], j[1], j[2], C, zero,
