@@ -295,8 +295,8 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
 // exact top-k threshold + mask / list emit
 // ------------------------------------------------------------------------------------------------------------
 // The (k+1)-th largest of each (head, query slice) row of s*Nk probs, k = min(n-1, topk), by an exact select over
-// the fp32 bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0). kThrParts workgroups share a
-// row. Each reads the row's top-12-bit histogram (built by scores_softmax_kernel), finds the bin that holds the
+// the fp32 bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0). kThrParts or more workgroups
+// share a row. Each reads the row's top-12-bit histogram (built by scores_softmax_kernel), finds the bin that holds the
 // threshold and its rank in the bin (all of them find the same), then scans its share of the row and gathers the
 // elements of that bin into the row's candidate area of the workspace. The candidates and the arrival count move
 // as relaxed agent-scope atomics (coherent stores and loads past this XCD's L2), ordered by the wait for the stores
@@ -305,7 +305,8 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
 // candidate area (e.g. the threshold falls on the exact zeros outside the local window) makes that last workgroup
 // run a full-row radix select from memory instead: exponent [30:23], then mantissa [22:15], [14:7], [6:0], with the
 // zeros counted by a wave ballot instead of 64 colliding LDS atomics.
-constexpr int kThrParts = 16;           // workgroups per (head, query slice) row
+constexpr int kThrParts = 16;           // workgroups per (head, query slice) row, at least (more for long rows)
+constexpr int kThrMaxParts = 64;
 constexpr int kThrThreads = 256;
 constexpr int kThrLdsCand = 16384;      // candidates the last workgroup holds in LDS
 constexpr int kCandPerBlock = 128;      // candidate words of the workspace per (head, query block)
@@ -437,7 +438,7 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
   // first, so one atomic per workgroup reserves its slots (a returning device-scope atomic per wave and step would
   // put a memory round trip on every step).
   if (gather) {
-    const int64_t per = (n + kThrParts - 1) / kThrParts;
+    const int64_t per = (n + (int)gridDim.x - 1) / (int)gridDim.x;
     const int64_t e0 = part * per, e1 = min<int64_t>(n, e0 + per);
     // a share of up to kThrRegs * kThrThreads elements is loaded into registers once (every load in flight at the
     // same time) and both counted and gathered from there; a larger share is read twice
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
   __syncthreads();
   if (tid == 0) s_arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (s_arrived != kThrParts - 1) return;   // workgroup-uniform
+  if (s_arrived != gridDim.x - 1) return;   // workgroup-uniform
 
   // 3. the last workgroup of the row
   unsigned prefix, rk;
@@ -643,7 +644,11 @@ int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices
                      unsigned* cand, float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt,
                      hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;
-  hipLaunchKernelGGL(topk_threshold_kernel, dim3(kThrParts, heads * q_slices), dim3(kThrThreads), 0, stream, probs,
+  // enough workgroups per row that each one's share fits its registers (kThrRegs elements per thread)
+  const int64_t row_n = (int64_t)(nq / q_slices) * nk;
+  const int parts = (int)std::min<int64_t>(kThrMaxParts, std::max<int64_t>(kThrParts,
+                                                             ceil_div(row_n, (int64_t)kThrRegs * kThrThreads)));
+  hipLaunchKernelGGL(topk_threshold_kernel, dim3(parts, heads * q_slices), dim3(kThrThreads), 0, stream, probs,
                      nq, nk, q_slices, topk, hist, cand, thr);
   FVSR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(topk_emit_kernel, dim3((heads * nq + 3) / 4), dim3(256), 0, stream, probs, thr, heads, nq, nk,
