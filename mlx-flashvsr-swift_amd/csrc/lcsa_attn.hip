@@ -699,7 +699,8 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
 // (shuffles) with one step across the waves. Up to kOrderLdsRows rows the lengths' bins and the sorted order stay in
 // LDS (kcnt is read once, the dealt order written once) and, while the waves' bitmaps fit together, every wave is
 // ranked in one pass (one bitmap segment per wave, one scan); beyond, the sorted order is staged in `order` itself
-// and the waves are ranked one after another.
+// and the waves are ranked one after another. When every list has the same length the row-id order is such an order
+// already and is dealt as it stands.
 constexpr int kOrderLdsRows = 8192;
 __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restrict__ kcnt, int rows, int nk_stride,
                                                           int dense, int grid, int32_t* __restrict__ order,
@@ -713,52 +714,73 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
   __shared__ int wpre[kWords];                                            // set bits in the words before word w
   __shared__ int lord[kOrderLdsRows];                                     // the sorted order (rows <= kOrderLdsRows)
   __shared__ uint8_t lbin[kOrderLdsRows];                                 // each row's bin (rows <= kOrderLdsRows)
-  __shared__ int s_longest;
+  __shared__ int s_longest, s_mixed;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool in_lds = rows <= kOrderLdsRows;
   int* const sorted = in_lds ? lord : order;
   if (tid < kBins) bin_start[tid] = 0;
-  if (tid == 0) s_longest = 0;
+  if (tid == 0) {
+    s_longest = 0;
+    s_mixed = 0;
+  }
   __syncthreads();
   auto list_len = [&](int r) -> int { return max(0, min(kcnt[r], nk_stride)); };
-  // the longest list (the lengths wait in lord until the sort overwrites it)
+  // the longest list, and whether the lengths differ at all (the lengths wait in lord until the sort overwrites it);
+  // a thread's loads are issued together, so their latencies overlap
   {
+    const int c0 = list_len(0);
     int m = 0;
-    for (int r = tid; r < rows; r += 1024) {
-      const int c = list_len(r);
-      if (in_lds) lord[r] = c;
-      m = max(m, c);
+    bool mixed = false;
+    for (int r0 = tid; r0 < rows; r0 += 4 * 1024) {
+      int c[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c[u] = list_len(min(r0 + u * 1024, rows - 1));   // loads without branches
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (r0 + u * 1024 < rows) {
+          if (in_lds) lord[r0 + u * 1024] = c[u];
+          m = max(m, c[u]);
+          mixed |= c[u] != c0;
+        }
+      }
     }
     for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o));
     if (lane == 0) atomicMax(&s_longest, m);
+    if (__ballot(mixed) != 0 && lane == 0) s_mixed = 1;
   }
   __syncthreads();
-  const int width = max(1, (s_longest + kBins - 2) / (kBins - 1));   // blocks per bin
-  auto bin_len = [&](int c) -> int {   // bin 0 = the longest lists
-    const int len = c <= 0 ? 0 : (dense ? 1 : min((c + width - 1) / width, kBins - 1));
-    return kBins - 1 - len;
-  };
-  auto bin_of = [&](int r) -> int { return bin_len(list_len(r)); };
-  for (int r = tid; r < rows; r += 1024) {
-    const int bn = in_lds ? bin_len(lord[r]) : bin_of(r);
-    if (in_lds) lbin[r] = (uint8_t)bn;
-    atomicAdd(&bin_start[bn], 1);
-  }
-  __syncthreads();
-  // exclusive scan of the 256 bin counts by waves 0..3
-  {
-    const int v = tid < kBins ? bin_start[tid] : 0;
-    const int incl = (int)wave_incl_scan((unsigned)v);
-    if (tid < kBins && lane == 63) wtot[wave] = incl;
-    __syncthreads();
-    if (tid < kBins) {
-      int base = 0;
-      for (int w = 0; w < wave; ++w) base += wtot[w];
-      bin_start[tid] = base + incl - v;
+  // every list of one length (the cross-attention's and the dense fallback's lists): the row-id order is already
+  // sorted by length and each of its waves by row id, so the sort and the ranking are skipped and the rows are dealt
+  // where they stand
+  const bool one_len = s_mixed == 0;
+  if (!one_len) {
+    const int width = max(1, (s_longest + kBins - 2) / (kBins - 1));   // blocks per bin
+    auto bin_len = [&](int c) -> int {   // bin 0 = the longest lists
+      const int len = c <= 0 ? 0 : (dense ? 1 : min((c + width - 1) / width, kBins - 1));
+      return kBins - 1 - len;
+    };
+    auto bin_of = [&](int r) -> int { return bin_len(list_len(r)); };
+    for (int r = tid; r < rows; r += 1024) {
+      const int bn = in_lds ? bin_len(lord[r]) : bin_of(r);
+      if (in_lds) lbin[r] = (uint8_t)bn;
+      atomicAdd(&bin_start[bn], 1);
     }
+    __syncthreads();
+    // exclusive scan of the 256 bin counts by waves 0..3
+    {
+      const int v = tid < kBins ? bin_start[tid] : 0;
+      const int incl = (int)wave_incl_scan((unsigned)v);
+      if (tid < kBins && lane == 63) wtot[wave] = incl;
+      __syncthreads();
+      if (tid < kBins) {
+        int base = 0;
+        for (int w = 0; w < wave; ++w) base += wtot[w];
+        bin_start[tid] = base + incl - v;
+      }
+    }
+    __syncthreads();
+    for (int r = tid; r < rows; r += 1024) sorted[atomicAdd(&bin_start[in_lds ? (int)lbin[r] : bin_of(r)], 1)] = r;
   }
-  __syncthreads();
-  for (int r = tid; r < rows; r += 1024) sorted[atomicAdd(&bin_start[in_lds ? (int)lbin[r] : bin_of(r)], 1)] = r;
   __threadfence_block();
   __syncthreads();
   grid = min(grid, kMaxPersistentWgs);
@@ -795,7 +817,12 @@ __global__ __launch_bounds__(1024) void attn_order_kernel(const int32_t* __restr
   };
   const int rwords = (rows + 31) / 32;
   const int nwaves = (rows + grid - 1) / grid;
-  if (in_lds && nwaves * rwords <= kWords) {
+  if (one_len) {
+    for (int p = tid; p < rows; p += 1024) {
+      const int w0 = p / grid * grid;
+      deal(w0, min(grid, rows - w0), p - w0, p);
+    }
+  } else if (in_lds && nwaves * rwords <= kWords) {
     // every wave at once: wave w's rows set their bits in bitmap segment w, one scan covers all segments
     for (int i = tid; i < nwaves * rwords; i += 1024) bm[i] = 0u;
     __syncthreads();
