@@ -22,7 +22,8 @@
 //                         bin, each workgroup gathers the bin's elements of its share of the row (held in
 //                         registers), and the last to arrive finishes the low 19 bits by three radix passes in LDS
 //                         (full-row 4-pass radix select when the bin is too large)
-//   topk_emit_kernel     one wave per query row: mask, selection bytes and compacted key lists (ballot + popcount)
+//   topk_emit_kernel     one wave per query row: mask, selection bytes and compacted key lists (ballot + popcount),
+//                        the row's probs loaded into registers at once
 #include "common.hpp"
 
 namespace fvsr {
@@ -542,7 +543,10 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
 
 // Mask, selection bytes and key lists from the row thresholds: one wave per query row (head, query block). Lists
 // hold the selected key blocks ascending, then the unselected ascending (argSort(!sel) of SparseAttention.swift:177
-// with a stable order).
+// with a stable order). A row of up to 64 * kEmitChunks key blocks is loaded into registers first, every load in
+// flight at once (the probs were just written on other XCDs, so each load waits on the memory-side cache); longer
+// rows are read chunk by chunk, twice.
+constexpr int kEmitChunks = 12;
 __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict__ probs,
                                                         const float* __restrict__ thr, int heads, int nq, int nk,
                                                         int q_slices, float* __restrict__ mask_out,
@@ -558,10 +562,10 @@ __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict_
   const int64_t roff = (int64_t)row * nk;
   const float* prow = probs + roff;
   int32_t* krow = kidx + roff;
-  int n_sel = 0;
-  for (int j0 = 0; j0 < nk; j0 += 64) {
+  // selected keys of chunk j0 (lanes j0 + lane < nk whose prob p is above the threshold) go to krow[n_sel ..]
+  auto emit_selected = [&](int j0, float p, int& n_sel) {
     const int j = j0 + lane;
-    const bool s = j < nk && prow[j] > th;
+    const bool s = j < nk && p > th;
     const uint64_t b = __ballot(s);
     if (s) krow[n_sel + __popcll(b & lt)] = j;
     if (j < nk) {
@@ -569,14 +573,30 @@ __global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict_
       if (mask_out) mask_out[roff + j] = s ? 1.f : 0.f;
     }
     n_sel += __popcll(b);
-  }
-  int n_un = n_sel;
-  for (int j0 = 0; j0 < nk; j0 += 64) {
+  };
+  auto emit_unselected = [&](int j0, float p, int& n_un) {
     const int j = j0 + lane;
-    const bool u = j < nk && !(prow[j] > th);
+    const bool u = j < nk && !(p > th);
     const uint64_t b = __ballot(u);
     if (u) krow[n_un + __popcll(b & lt)] = j;
     n_un += __popcll(b);
+  };
+  int n_sel = 0, n_un;
+  if (nk <= 64 * kEmitChunks) {
+    float pv[kEmitChunks];
+#pragma unroll
+    for (int c = 0; c < kEmitChunks; ++c) pv[c] = prow[min(64 * c + lane, nk - 1)];   // no branch between loads
+#pragma unroll
+    for (int c = 0; c < kEmitChunks; ++c)
+      if (64 * c < nk) emit_selected(64 * c, pv[c], n_sel);
+    n_un = n_sel;
+#pragma unroll
+    for (int c = 0; c < kEmitChunks; ++c)
+      if (64 * c < nk) emit_unselected(64 * c, pv[c], n_un);
+  } else {
+    for (int j0 = 0; j0 < nk; j0 += 64) emit_selected(j0, j0 + lane < nk ? prow[j0 + lane] : 0.f, n_sel);
+    n_un = n_sel;
+    for (int j0 = 0; j0 < nk; j0 += 64) emit_unselected(j0, j0 + lane < nk ? prow[j0 + lane] : 0.f, n_un);
   }
   if (lane == 0) kcnt[row] = n_sel;
 }
