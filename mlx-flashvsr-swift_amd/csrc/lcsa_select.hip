@@ -162,15 +162,6 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
   const int tid = threadIdx.x;
   const int sq = nq / q_slices;                 // query blocks per slice
   const int t_first = i0 / sq;
-  for (int e = tid; e < kScoreRows * kHeadDim; e += kScoreThreads) {
-    const int r = e / kHeadDim, d = e % kHeadDim;
-    qs[e] = (i0 + r < nq) ? pq[(int64_t)(i0 + r) * C + h * kHeadDim + d] : 0.f;
-  }
-  for (int e = tid; e < kScoreRows * sw; e += kScoreThreads) {
-    const int r = e / sw, c = e - r * sw;
-    lm[e] = local[((i0 + r) % s) * s + c];
-  }
-  __syncthreads();
   const float sqrt_d = sqrtf((float)kHeadDim);
   // Key blocks in chunks of 64, the two halves of the workgroup on alternate chunks (half 0: chunks 0, 2, ..; half
   // 1: chunks 1, 3, ..) with a staging buffer each: the chunk's pooled-key rows (64 x 512 B) are read with coalesced
@@ -186,12 +177,13 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
   const float* kbase = pk + h * kHeadDim;
   float* kst = ks + half * kKeyChunk * kKStride;
   constexpr int kLoads = kKeyChunk * (kHeadDim / 4) / 256;   // 16-byte loads per thread of a half per chunk
+  // every call issues the same kLoads loads (key blocks past nk read block nk - 1, which is never stored), so the
+  // compiler can count the first chunks' loads and store the queries before they land
   auto load_chunk = [&](f32x4 (&pre)[kLoads], int j0) {
-    const int nj = min(kKeyChunk, nk - j0);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int e = i * 256 + htid, jj = e >> 5, c4 = e & 31;
-      if (jj < nj) pre[i] = *(const f32x4*)(kbase + (kmap.row(j0 + jj) / kBlock) * C + 4 * c4);
+      pre[i] = *(const f32x4*)(kbase + (kmap.row(min(j0 + jj, nk - 1)) / kBlock) * C + 4 * c4);
     }
   };
   // this lane's A operands, read from LDS at each step: query row li, dims 32 lg .. 32 lg + 31 (lanes li >= 8 read
@@ -207,7 +199,7 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
       if (jj < nj) *(f32x4*)(kst + jj * kKStride + 4 * c4) = pre[i];
     }
     __syncthreads();
-    if (j_next < nk) load_chunk(pre, j_next);
+    if (j_next < nk) load_chunk(pre, j_next);   // no loads past the last chunk
     if (16 * hw < nj) {   // wave-uniform; rows of keys past nj hold stale data and are not stored
       const float* krow = kst + (16 * hw + li) * kKStride + 32 * lg;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -236,10 +228,36 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
   f32x4 pre[kChunksInFlight][kLoads];
   const int rounds = (nk + 2 * kKeyChunk - 1) / (2 * kKeyChunk);
   auto chunk_of = [&](int r) { return (2 * r + half) * kKeyChunk; };
-  static_for<0, kChunksInFlight>([&](auto d_c) {
-    constexpr int D = decltype(d_c)::value;
-    if (chunk_of(D) < nk) load_chunk(pre[D], chunk_of(D));
-  });
+  // the group's pooled queries (two floats per thread) and local-window bytes are loaded first, then the first chunks:
+  // loads complete in order, so the queries and bytes can be stored to LDS while the chunks are still in flight (rows
+  // past nq read row nq - 1 and store zeros; indices are clamped rather than branched around, so the compiler can
+  // count the loads)
+  static_assert(kScoreRows * kHeadDim == 2 * kScoreThreads, "two query floats per thread");
+  const int qr = 2 * tid / kHeadDim, qd = 2 * tid % kHeadDim;
+  const float2 qv = *(const float2*)(pq + (int64_t)min(i0 + qr, nq - 1) * C + h * kHeadDim + qd);
+  constexpr int kLmRegs = 4;   // local-window bytes per thread held at once: one pass up to 256 columns
+  const int nlm = kScoreRows * sw;
+  const bool lm_regs = nlm <= kLmRegs * kScoreThreads;
+  auto lm_byte = [&](int e) {
+    const int rr = e / sw, c = e - rr * sw;
+    return local[((i0 + rr) % s) * s + c];
+  };
+  unsigned lv[kLmRegs];   // a register each: packing the bytes would wait for their loads before the chunks' issue
+  if (lm_regs) {
+#pragma unroll
+    for (int u = 0; u < kLmRegs; ++u) lv[u] = lm_byte(min(u * kScoreThreads + tid, nlm - 1));
+  } else {
+    for (int e = tid; e < nlm; e += kScoreThreads) lm[e] = lm_byte(e);
+  }
+  static_for<0, kChunksInFlight>([&](auto d_c) { load_chunk(pre[decltype(d_c)::value], chunk_of(decltype(d_c)::value)); });
+  if (lm_regs) {
+#pragma unroll
+    for (int u = 0; u < kLmRegs; ++u)
+      if (u * kScoreThreads + tid < nlm) lm[u * kScoreThreads + tid] = (uint8_t)lv[u];
+  }
+  qs[2 * tid] = i0 + qr < nq ? qv.x : 0.f;
+  qs[2 * tid + 1] = i0 + qr < nq ? qv.y : 0.f;
+  __syncthreads();
   for (int r0 = 0; r0 < rounds; r0 += kChunksInFlight) {
     static_for<0, kChunksInFlight>([&](auto d_c) {
       constexpr int D = decltype(d_c)::value;
