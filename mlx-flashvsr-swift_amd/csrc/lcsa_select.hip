@@ -387,8 +387,10 @@ __device__ __forceinline__ void radix_digit(unsigned (&hist)[kThrThreads / 64][2
   rank = *s_rank;
 }
 
+// per: the elements of a row each workgroup scans, ceil(sq * nk / gridDim.x) (a host-side division: a 64-bit divide
+// here would put branches between the histogram's loads and the share's)
 __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float* __restrict__ probs, int nq,
-                                                                     int nk, int q_slices, int topk,
+                                                                     int nk, int q_slices, int topk, int64_t per,
                                                                      unsigned* __restrict__ hist12,
                                                                      unsigned* __restrict__ cand_ws,
                                                                      float* __restrict__ thr_out) {
@@ -422,6 +424,19 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
     hv[4 * i + 1] = x[1];
     hv[4 * i + 2] = x[2];
     hv[4 * i + 3] = x[3];
+  }
+  // this workgroup's share of the row: up to kThrRegs * kThrThreads elements are loaded into registers here, every
+  // load in flight with the histogram's (they do not depend on the bin; indices are clamped rather than branched
+  // around, so the histogram can be waited for alone), and both counted and gathered from there in step 2; a larger
+  // share is read twice there
+  const int64_t e0 = part * per, e1 = min<int64_t>(n, e0 + per);
+  const bool in_regs = per <= (int64_t)kThrRegs * kThrThreads;
+  unsigned rv[kThrRegs];   // loaded even when unused (a larger share): a branch here would drain the histogram's
+                           // loads and these together
+#pragma unroll
+  for (int i = 0; i < kThrRegs; ++i) {
+    const int64_t e = e0 + tid + (int64_t)i * kThrThreads;
+    rv[i] = bits[min(e, n - 1)];   // entries past the share are masked where they are used (in_share)
   }
   unsigned psum = 0;
 #pragma unroll
@@ -457,21 +472,11 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
   // first, so one atomic per workgroup reserves its slots (a returning device-scope atomic per wave and step would
   // put a memory round trip on every step).
   if (gather) {
-    const int64_t per = (n + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int64_t e0 = part * per, e1 = min<int64_t>(n, e0 + per);
-    // a share of up to kThrRegs * kThrThreads elements is loaded into registers once (every load in flight at the
-    // same time) and both counted and gathered from there; a larger share is read twice
-    const bool in_regs = per <= (int64_t)kThrRegs * kThrThreads;
-    unsigned rv[kThrRegs];
+    auto in_share = [&](int i) { return e0 + tid + (int64_t)i * kThrThreads < e1; };
     unsigned mine = 0;
     if (in_regs) {
 #pragma unroll
-      for (int i = 0; i < kThrRegs; ++i) {
-        const int64_t e = e0 + tid + (int64_t)i * kThrThreads;
-        rv[i] = e < e1 ? bits[e] : 0xffffffffu;   // all-ones: outside every bin of a prob in [0, 1]
-      }
-#pragma unroll
-      for (int i = 0; i < kThrRegs; ++i) mine += (rv[i] >> 19) == bin ? 1u : 0u;
+      for (int i = 0; i < kThrRegs; ++i) mine += (rv[i] >> 19) == bin && in_share(i) ? 1u : 0u;
     } else {
       for (int64_t e = e0 + tid; e < e1; e += kThrThreads) mine += (bits[e] >> 19) == bin ? 1u : 0u;
     }
@@ -492,7 +497,7 @@ __global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float
       if (in_regs) {
 #pragma unroll
         for (int i = 0; i < kThrRegs; ++i) {
-          if ((rv[i] >> 19) == bin) {
+          if ((rv[i] >> 19) == bin && in_share(i)) {
             if (at < cap) __hip_atomic_store(cw + at, rv[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ++at;
           }
@@ -687,7 +692,7 @@ int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices
   const int parts = (int)std::min<int64_t>(kThrMaxParts, std::max<int64_t>(kThrParts,
                                                              ceil_div(row_n, (int64_t)kThrRegs * kThrThreads)));
   hipLaunchKernelGGL(topk_threshold_kernel, dim3(parts, heads * q_slices), dim3(kThrThreads), 0, stream, probs,
-                     nq, nk, q_slices, topk, hist, cand, thr);
+                     nq, nk, q_slices, topk, ceil_div(row_n, (int64_t)parts), hist, cand, thr);
   FVSR_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(topk_emit_kernel, dim3((heads * nq + 3) / 4), dim3(256), 0, stream, probs, thr, heads, nq, nk,
                      q_slices, mask_out, sel, kidx, kcnt);
