@@ -197,3 +197,26 @@ def test_select_rejects_uneven_slices(dev):
     with pytest.raises(fvsr_lcsa.FVSRError) as ei:
         fvsr_lcsa.draft_block_mask(q, k, 1, 2, 2, np.ones((2, 2), bool), 1)
     assert ei.value.status == 1
+
+
+def test_long_rows_take_the_streaming_paths(dev):
+    """One head, 300 blocks per slice, 300 query x 1200 key blocks: rows longer than the emit kernel keeps in
+    registers (768 key blocks), a local window wider than the scores kernel's one-pass byte staging (256 columns) and
+    a (head, slice) row of 360,000 probs, more than 64 threshold workgroups hold in registers (each then reads its
+    share twice). Block means with a wide spread (+ token noise) keep the probabilities apart, so the mask is
+    checked as every other: bit-exact where the threshold has a margin, the near-tie rule elsewhere."""
+    g = torch.Generator().manual_seed(7)
+    s, nq, nk = 300, 300, 1200
+    qb = 3.0 * torch.randn((nq, 1, 128), generator=g)
+    kb = 3.0 * torch.randn((nk, 1, 128), generator=g)
+    q = (qb + torch.randn((nq, 128, 128), generator=g)).reshape(-1, 128)
+    k = (kb + torch.randn((nk, 128, 128), generator=g)).reshape(-1, 128)
+    yy, xx = np.divmod(np.arange(s), 20)   # a 15 x 20 block grid, local range 7
+    local = (np.abs(yy[:, None] - yy[None, :]) <= 3) & (np.abs(xx[:, None] - xx[None, :]) <= 3)
+    topk = 20000   # of 47,616 in-window pairs
+    ref_mask, ref_probs = O.draft_block_mask_and_probs(q.numpy(), k.numpy(), 1, 1, s, local, topk)
+    mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q.to(dev), k.to(dev), 1, 1, s, local, topk)
+    assert O.compare(probs.cpu().numpy(), ref_probs)["rel"] <= 1e-5
+    check_mask(mask, ref_mask, ref_probs, 1, topk)
+    check_lists(mask, kidx, kcnt)
+    assert int(kcnt.sum()) == int(ref_mask.sum())
