@@ -13,7 +13,8 @@
 //                        quarters sum one run of 32 tokens each (coalesced 16-byte loads, fp32), the runs meet in
 //                        LDS and the block mean ((r0 + r1) + (r2 + r3)) / n is stored (Q and K, or Q and the new
 //                        ring keys, in one launch); the launch also clears the histogram below
-//   scores_softmax_kernel one 8-wave workgroup per (8 query blocks, head): pooled-key rows staged through LDS in
+//   scores_softmax_kernel one 8-wave workgroup per (8 query blocks, head), a head's workgroups on one XCD (its L2
+//                         serves their pooled keys): pooled-key rows staged through LDS in
 //                         coalesced chunks of 64 keys, two chunks side by side, read once per 8 query rows; scores
 //                         + local mask in LDS, one wave per row for max / exp / sum / normalise; it also counts the
 //                         nonzero probs of each (head, query slice) per top-12-bit bin
@@ -157,8 +158,12 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
   float* ss = ks + 2 * kKeyChunk * kKStride;           // [kScoreRows][nk]
   const int sw = min(s, nk);                           // local-window columns that key blocks 0..nk-1 use
   uint8_t* lm = (uint8_t*)(ss + kScoreRows * nk);      // [kScoreRows][sw] local-window bytes of this group's rows
-  const int h = blockIdx.y;
-  const int i0 = blockIdx.x * kScoreRows;
+  // (head, query group) from the XCD-remapped workgroup index, head-major: each XCD's L2 then serves the pooled keys
+  // of one or two heads to all of its workgroups, instead of every head's to a few of each
+  const int ngroups = (nq + kScoreRows - 1) / kScoreRows;
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = lid / ngroups;
+  const int i0 = (lid - h * ngroups) * kScoreRows;
   const int tid = threadIdx.x;
   const int sq = nq / q_slices;                 // query blocks per slice
   const int t_first = i0 / sq;
@@ -665,7 +670,7 @@ size_t scores_smem_bytes(int nk, int s) {
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
                           const uint8_t* local, float* probs, unsigned* hist, int q_slices, hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;
-  dim3 grid((nq + kScoreRows - 1) / kScoreRows, heads);
+  dim3 grid((unsigned)(ceil_div(nq, kScoreRows) * heads));   // (head, query group), remapped by XCD in the kernel
   const size_t smem = scores_smem_bytes(nk, s);
   if (smem > 160 * 1024)
     return set_error(FVSR_ERR_UNSUPPORTED, "scores stage: too many key blocks for LDS");
