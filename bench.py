@@ -26,7 +26,9 @@ for p in (PKG, ROOT):
         sys.path.insert(0, p)
 
 METRIC = "block-sparse attn ms/layer-call + effective TFLOP/s (% MFMA peak), 1920×1152"
+HEADLINE = "sparse_1920x1152_bf16"   # the workload METRIC is quoted on; its PMC summary holds the traffic figure
 PEAK_BF16_TFLOPS = 2500.0            # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3             # MI355X dense fp32 MFMA (the fp32 lane's v_mfma_f32_32x32x2_f32)
 PROFILE_PMC = os.path.join(ROOT, "profiles", "lcsa_attn_bf16_1920x1152_pmc.txt")
 
 
@@ -41,7 +43,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps first (default: 300 layer calls, ~0.2 s, so the part's clock has settled "
                          "before timing; 20 for the other modes, whose warm-up already runs that long)")
-    ap.add_argument("--workload", default="sparse_1920x1152_bf16")
+    ap.add_argument("--workload", default=HEADLINE)
     ap.add_argument("--seed", type=int, default=None, help="generator seed (default: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -613,9 +615,13 @@ def main():
 
     achieved = kept / (ms_attn * 1e-3) / 1e12
     value = kept / (ms_step * 1e-3) / 1e12
-    traffic = read_traffic()
+    fp32 = wl.dtype == torch.float32
+    peak = PEAK_FP32_TFLOPS if fp32 else PEAK_BF16_TFLOPS
+    # the committed PMC summary covers the headline workload's kernel only
+    traffic = read_traffic() if wl.name == HEADLINE else None
+    res = f"{wl.width}×{wl.height}"
     line = {
-        "metric": METRIC,
+        "metric": METRIC if wl.name == HEADLINE else METRIC.replace("1920×1152", res),
         "value": round(value, 2),
         "unit": "TFLOP/s (effective, kept blocks; whole layer call = selection + attention)",
         "n_gpus": 1,
@@ -625,7 +631,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp32" if fp32 else "bf16",
         "data": (f"synthetic, seed {seed} ({'smooth field + noise, ' if wl.smooth else 'i.i.d. N(0,1), '}"
                  "per-head RMS norm + 3-D RoPE on Q/K; no checkpoint)"),
         "config": {
@@ -645,7 +651,7 @@ def main():
             "dense_masked_walk": round(ms_masked, 4),
         },
         "attention_tflops": round(achieved, 2),
-        "layer_call_frac": round(value / PEAK_BF16_TFLOPS, 4),
+        "layer_call_frac": round(value / peak, 4),
         "sparse_vs_dense_speedup": round(ms_dense / ms_attn, 3),
         "layer_call_vs_dense_speedup": round(ms_dense / ms_step, 3),
         "sparse_vs_masked_walk_speedup": round(ms_masked / ms_attn, 3),
@@ -653,9 +659,9 @@ def main():
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
+            "peak": peak,
             "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "frac": round(achieved / peak, 4),
             "traffic": traffic,
             "traffic_source": (f"{os.path.relpath(PROFILE_PMC, ROOT)}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of "
                                "the sparse attention kernel, copy-calibrated (not measured in this run)"
