@@ -372,3 +372,56 @@ def test_64_query_waves_equal_32_query_waves(dev, tmp_path):
     assert np.array_equal(z["o"], _np(o))
     assert np.array_equal(z["od"], _np(od))
     assert torch.equal(o, od)
+
+
+def _rows_vs_torch(q, k, v, m, heads, o, pairs):
+    """Worst rel of the GPU output against a float32 torch softmax over the listed key blocks of a few rows."""
+    worst = 0.0
+    for h, i in pairs:
+        blocks = m[h, i].nonzero().flatten().tolist()
+        got = o[i * 128:(i + 1) * 128, h * 128:(h + 1) * 128].float()
+        if not blocks:
+            assert (got == 0).all()
+            continue
+        qs = q[i * 128:(i + 1) * 128, h * 128:(h + 1) * 128].float()
+        rows = torch.cat([torch.arange(j * 128, min((j + 1) * 128, k.shape[0]), device=k.device) for j in blocks])
+        ks, vs = k[rows, h * 128:(h + 1) * 128].float(), v[rows, h * 128:(h + 1) * 128].float()
+        ref = torch.softmax(qs @ ks.t() / 128 ** 0.5, dim=-1) @ vs
+        worst = max(worst, float((got - ref).abs().max() / ref.abs().max()))
+    return worst
+
+
+@pytest.mark.parametrize("heads,lqb,uniform", [(2, 4200, False), (2, 4200, True), (1, 140000, False),
+                                               (1, 140000, True)])
+def test_row_counts_beyond_the_order_kernels_lds(dev, heads, lqb, uniform):
+    """More rows than the row-order kernel keeps in LDS (8192: the sorted order is staged in the workspace) and, at
+    140,000 rows, more than its row-id bitmap covers (131,072: each wave is ranked by scanning its rows). Lists of
+    mixed lengths (0 .. 4 blocks) and of one length (2 blocks each: the order is dealt without the sort). Outputs
+    start as NaN, so a row the walk skipped fails; kernel == dense fallback everywhere, empty rows are zeros, and a
+    few rows match a float32 torch softmax."""
+    lk = 3 * 128 + 50
+    g = torch.Generator(device=dev).manual_seed(lqb + int(uniform))
+    q = torch.randn((lqb * 128, heads * 128), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((lk, heads * 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((lk, heads * 128), generator=g, device=dev).to(torch.bfloat16)
+    if uniform:
+        m = torch.zeros((heads, lqb, 4), device=dev)
+        m[..., 1] = 1.0
+        m[..., 3] = 1.0
+    else:
+        dens = torch.rand((heads, lqb, 1), generator=g, device=dev)
+        m = (torch.rand((heads, lqb, 4), generator=g, device=dev) < dens).float()
+    o = torch.full((lqb * 128, heads * 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    od = torch.full_like(o, float("nan"))
+    print(f"  rows {heads * lqb}, kept blocks {int(m.sum())}", flush=True)
+    fvsr_lcsa.kernel_block_attention(q, k, v, m, heads, out=o)
+    fvsr_lcsa.block_masked_attention(q, k, v, m, heads, out=od)
+    torch.cuda.synchronize()
+    assert not torch.isnan(o).any()
+    assert torch.equal(o, od)
+    empty = (m.sum(-1) == 0).nonzero().tolist()
+    ov = o.view(lqb, 128, heads, 128)
+    for h, i in empty[:64]:
+        assert (ov[i, :, h] == 0).all()
+    pairs = [(h, i) for h in range(heads) for i in (0, 1, lqb // 2, lqb - 2, lqb - 1)]
+    assert _rows_vs_torch(q, k, v, m, heads, o, pairs) <= BF16_REL
