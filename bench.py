@@ -72,6 +72,9 @@ def parse_args():
                     help="run only a plain copy of known size (the window-partition kernel over 16x72x120 bf16 "
                          "tokens of 1536 channels: 424.7 MB read + 424.7 MB written per launch), the reference "
                          "point that scales the FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="time only a plain bf16 GEMM (torch.matmul on hipBLASLt, 8192^3 and 16384^3, N(0,1) data): "
+                         "the practical MFMA rate of these parts, beside which the attention's rate is read")
     return ap.parse_args()
 
 
@@ -179,6 +182,30 @@ def copy_calibration(steps: int):
     ms = e0.elapsed_time(e1) / steps
     print(json.dumps({"copy_calibration": {"bytes_read": nbytes, "bytes_written": nbytes, "ms": round(ms, 4),
                                            "GB/s": round(2 * nbytes / ms / 1e6, 1)}}), flush=True)
+
+
+def gemm_ceiling(steps: int):
+    """The best plain bf16 GEMM the library stack reaches on this part (torch.matmul -> hipBLASLt)."""
+    import torch
+
+    out = {}
+    for n in (8192, 16384):
+        a = torch.randn((n, n), device="cuda:0", dtype=torch.bfloat16)
+        b = torch.randn((n, n), device="cuda:0", dtype=torch.bfloat16)
+        for _ in range(3):
+            c = a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(1, steps)
+        e0.record()
+        for _ in range(reps):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[f"{n}^3"] = {"ms": round(ms, 4), "TFLOP/s": round(2 * n ** 3 / (ms * 1e-3) / 1e12, 1)}
+        del a, b, c
+    print(json.dumps({"gemm_ceiling": out}), flush=True)
 
 
 def stream_bench(args):
@@ -505,6 +532,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.gemm_ceiling:
+        gemm_ceiling(args.steps)
         return
     if args.stream and args.full_blocks:
         stream_blocks_bench(args)
