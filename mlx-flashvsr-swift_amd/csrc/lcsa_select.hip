@@ -258,7 +258,10 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
     });
   }
   __syncthreads();
-  for (int e = tid; e < 2 * kHistBins; e += kScoreThreads) lhist[e] = 0u;
+  // the group's rows fall in one or two query slices: clear the histograms they use
+  const int t_last = min(q_slices - 1, (min(i0 + kScoreRows, nq) - 1) / sq);
+  const int nlh = min(2, t_last - t_first + 1);
+  for (int e = tid; e < nlh * kHistBins; e += kScoreThreads) lhist[e] = 0u;
   __syncthreads();
   for (int r = wave; r < kScoreRows; r += kScoreThreads / 64) {
     if (i0 + r >= nq) break;
@@ -293,7 +296,6 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
   }
   __syncthreads();
   // flush the nonzero bins of the workgroup histograms
-  const int t_last = min(q_slices - 1, (min(i0 + kScoreRows, nq) - 1) / sq);
   for (int dt = 0; dt < 2 && t_first + dt <= t_last; ++dt) {
     unsigned* g = hist + ((int64_t)h * q_slices + t_first + dt) * kHistBins;
     for (int bn = tid; bn < kHistBins; bn += kScoreThreads) {
