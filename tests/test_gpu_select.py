@@ -220,3 +220,26 @@ def test_long_rows_take_the_streaming_paths(dev):
     check_mask(mask, ref_mask, ref_probs, 1, topk)
     check_lists(mask, kidx, kcnt)
     assert int(kcnt.sum()) == int(ref_mask.sum())
+
+
+def test_threshold_on_exact_ties_in_a_large_bin(dev):
+    """Sixteen query blocks with zero queries score every key block alike, so their 5408 probs tie at exactly 1/338
+    and the (k+1)-th largest (k = 3000, with 2109 probs above the tie) falls on them: the threshold's bin holds 5442
+    candidates, most of them in the shares of the row's first two workgroups. The mask keeps the 2109 probs strictly
+    above the tie, as the oracle's."""
+    g = torch.Generator().manual_seed(3)
+    s, nq, nk = 135, 135, 338
+    q = torch.randn((nq, 128, 128), generator=g) + 2.0 * torch.randn((nq, 1, 128), generator=g)
+    k = torch.randn((nk, 128, 128), generator=g) + 2.0 * torch.randn((nk, 1, 128), generator=g)
+    q[:16] = 0.0
+    q, k = q.reshape(-1, 128), k.reshape(-1, 128)
+    local = np.ones((s, s), dtype=bool)
+    topk = 3000
+    ref_mask, ref_probs = O.draft_block_mask_and_probs(q.numpy(), k.numpy(), 1, 1, s, local, topk)
+    tie = np.float32(1.0) / np.float32(nk)
+    assert int((ref_probs == tie).sum()) == 16 * nk and int((ref_probs > tie).sum()) < topk + 1
+    mask, probs, kidx, kcnt = fvsr_lcsa.draft_block_mask_and_probs(q.to(dev), k.to(dev), 1, 1, s, local, topk)
+    assert O.compare(probs.cpu().numpy(), ref_probs)["rel"] <= 1e-5
+    check_mask(mask, ref_mask, ref_probs, 1, topk)
+    check_lists(mask, kidx, kcnt)
+    assert int(mask.sum()) == int((ref_probs > tie).sum())
