@@ -228,25 +228,25 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
   static_assert(kScoreRows * kHeadDim == 2 * kScoreThreads, "two query floats per thread");
   const int qr = 2 * tid / kHeadDim, qd = 2 * tid % kHeadDim;
   const float2 qv = *(const float2*)(pq + (int64_t)min(i0 + qr, nq - 1) * C + h * kHeadDim + qd);
-  constexpr int kLmRegs = 4;   // local-window bytes per thread held at once: one pass up to 256 columns
-  const int nlm = kScoreRows * sw;
-  const bool lm_regs = nlm <= kLmRegs * kScoreThreads;
-  auto lm_byte = [&](int e) {
-    const int rr = e / sw, c = e - rr * sw;
-    return local[((i0 + rr) % s) * s + c];
-  };
+  // local-window bytes: wave r stages row r (its local row (i0 + r) mod s), lane c0 its columns c0 + 64 u; no
+  // division per byte
+  constexpr int kLmRegs = 4;   // columns per lane held at once: one pass up to 256 columns
+  static_assert(kScoreThreads == 64 * kScoreRows, "one wave per local-window row");
+  const bool lm_regs = sw <= 64 * kLmRegs;
+  const uint8_t* const lrow = local + (int64_t)((i0 + wave) % s) * s;
+  uint8_t* const lmrow = lm + wave * sw;
   unsigned lv[kLmRegs];   // a register each: packing the bytes would wait for their loads before the chunks' issue
   if (lm_regs) {
 #pragma unroll
-    for (int u = 0; u < kLmRegs; ++u) lv[u] = lm_byte(min(u * kScoreThreads + tid, nlm - 1));
+    for (int u = 0; u < kLmRegs; ++u) lv[u] = lrow[min(lane + 64 * u, sw - 1)];
   } else {
-    for (int e = tid; e < nlm; e += kScoreThreads) lm[e] = lm_byte(e);
+    for (int c = lane; c < sw; c += 64) lmrow[c] = lrow[c];
   }
   static_for<0, kChunksInFlight>([&](auto d_c) { load_chunk(pre[decltype(d_c)::value], chunk_of(decltype(d_c)::value)); });
   if (lm_regs) {
 #pragma unroll
     for (int u = 0; u < kLmRegs; ++u)
-      if (u * kScoreThreads + tid < nlm) lm[u * kScoreThreads + tid] = (uint8_t)lv[u];
+      if (lane + 64 * u < sw) lmrow[lane + 64 * u] = (uint8_t)lv[u];
   }
   qs[2 * tid] = i0 + qr < nq ? qv.x : 0.f;
   qs[2 * tid + 1] = i0 + qr < nq ? qv.y : 0.f;
