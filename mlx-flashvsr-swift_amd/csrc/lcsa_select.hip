@@ -123,7 +123,9 @@ __device__ __forceinline__ void wave_hist_add(unsigned* h, unsigned key, bool va
 constexpr int kScoreRows = 8;   // query blocks per workgroup (one per wave in the softmax)
 constexpr int kScoreThreads = 512;   // 8 waves: two halves of 4 stage alternate key chunks side by side
 constexpr int kKeyChunk = 64;   // key blocks staged in LDS at a time by one half
-constexpr int kChunksInFlight = 3;   // chunk loads each half keeps in flight (registers)
+constexpr int kChunksInFlight = 1;   // chunk loads each half keeps in flight (registers): with the two halves
+                                     // alternating, one is enough; 92 VGPRs (2 took 118 and ran 3 % slower, 3 took
+                                     // 159 and 8 % slower, 4 slower still)
 constexpr int kKStride = kHeadDim + 4;   // padded LDS row of a pooled key (floats)
 constexpr int kHistBins = 4096; // top-12-bit bins (bits 30..19) of the prob bit patterns
 
