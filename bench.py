@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -47,6 +48,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=None, help="generator seed (default: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU oracle sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-stream", action="store_true",
+                    help="leave out the streaming-stack figures (30 layers from the projections) of the default line")
     ap.add_argument("--attn-only", action="store_true",
                     help="profiling: run only the sparse attention launches (one selection up front) and print a "
                          "summary line instead of the benchmark line")
@@ -145,6 +148,25 @@ def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
         return 4.0 * 128 * min(128, wl.lq - i * 128) * keys
     sample_flops = sum(row_flops(h, i) for h, i in done)
     t_layer = t_sel + t_att * kept_flops_total / max(sample_flops, 1.0)
+    # the reference's own CPU path (blockMaskedAttention, DiT.swift:279-313): SDPA of a query block over EVERY key
+    # under the expanded boolean mask, so its cost does not depend on the selection; a few rows, scaled to all rows
+    d = 128
+    t_dense, n_dense = 0.0, 0
+    for idx in order[:96]:
+        h, i = rows[idx]
+        t0 = time.perf_counter()
+        qh = qn[i * 128:(i + 1) * 128, h * d:(h + 1) * d]
+        sc = (qh @ kn[:, h * d:(h + 1) * d].T) * np.float32(1.0 / math.sqrt(d))
+        keep = np.repeat(m[h, i] > 0.5, 128)[: wl.lk]
+        sc[:, ~keep] = -np.inf
+        if keep.any():
+            sc = np.exp(sc - sc.max(axis=1, keepdims=True))
+            o_row = (sc / sc.sum(axis=1, keepdims=True)) @ vn[:, h * d:(h + 1) * d]
+        t_dense += time.perf_counter() - t0
+        n_dense += 1
+        if t_dense >= 3.0:
+            break
+    t_dense_layer = t_sel + t_dense * len(rows) / max(n_dense, 1)
     threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
     return {
         "value": kept_flops_total / t_layer / 1e12,
@@ -158,6 +180,13 @@ def cpu_baseline(wl, q, k, v, mask, kept_flops_total, budget_s):
                   f"per-row masked attention over the selected key blocks of {len(done)} of {len(rows)} (head, "
                   f"query block) rows ({t_att:.2f} s), scaled by kept FLOPs",
         "mask_equals_gpu": mask_equal,
+        "reference_dense_path": {
+            "ms_per_layer_call": round(t_dense_layer * 1e3, 1),
+            "tflops_effective_kept": round(kept_flops_total / t_dense_layer / 1e12, 4),
+            "sample": f"the selection as above + masked SDPA of a query block over all {wl.lk} keys (the "
+                      f"reference's blockMaskedAttention CPU path) on {n_dense} rows ({t_dense:.2f} s), scaled by "
+                      f"row count",
+        },
     }
 
 
@@ -208,15 +237,16 @@ def gemm_ceiling(steps: int):
     print(json.dumps({"gemm_ceiling": out}), flush=True)
 
 
-def stream_bench(args):
+def stream_measure(layers: int, reps: int, warm_runs: int, seed: int, iid: bool, proj: bool, split: bool):
     """The attention stack of the streaming DiT at 1920x1152 (the reference's geometry: s = 135 blocks per slice, a
     first chunk of 6 latent frames = 3 slices, then chunks of 2 latent frames = 1 slice; KV window 3 slices;
     default top-k 16199, local range 11; Pipeline.swift:22-23,68,95-102; DiT.swift:478-538). Each layer call runs
-    append + select + block-sparse attention + evict through fvsr_lcsa_layer. Q/K/V of each chunk are synthetic,
-    resident in HBM and shared by the layers: by default Q/K are a smooth field over the 14 latent frames plus noise
-    (with --from-projections: WanRMSNorm weights of about 2, so the pooled scores of a row span a wide range, as
-    for real features); --iid draws them N(0,1). Without --from-projections Q/K are per-head RMS-normed with 3-D
-    RoPE at the chunk's latent frames."""
+    append + select + block-sparse attention + evict through fvsr_lcsa_layer (fvsr_lcsa_layer_qkv with `proj`).
+    Q/K/V of each chunk are synthetic, resident in HBM and shared by the layers: by default Q/K are a smooth field
+    over the 14 latent frames plus noise (with `proj`: WanRMSNorm weights of about 2, so the pooled scores of a row
+    span a wide range, as for real features); `iid` draws them N(0,1). Without `proj` Q/K are per-head RMS-normed
+    with 3-D RoPE at the chunk's latent frames. With `split`, the selection and the attention of one steady layer
+    call are also timed apart (on the last layer's ring, the new slice appended, back to back). Returns a dict."""
     import torch
 
     import fvsr_lcsa
@@ -229,12 +259,11 @@ def stream_bench(args):
     local = fvsr_lcsa.local_block_mask(bh, bw, 11)
     topk = synth.step_topk(s, synth.default_topk_ratio(1152, 1920))
     chunks = [(3, 0), (1, 6), (1, 8), (1, 10), (1, 12)]   # (slices, first latent frame)
-    gen = torch.Generator(device=dev).manual_seed(args.seed or 0)
+    gen = torch.Generator(device=dev).manual_seed(seed)
     data = []
-    proj = args.from_projections
-    smooth = not args.iid
+    smooth = not iid
     if smooth:
-        cgen = torch.Generator().manual_seed(args.seed or 0)
+        cgen = torch.Generator().manual_seed(seed)
         field = synth.smooth_field(14, lat_h, lat_w, C, cgen)
         wscale = 2.0
     else:
@@ -259,7 +288,9 @@ def stream_bench(args):
         k = synth.rope_apply(synth.rms_norm(k, H), H, cos, sin)
         data.append(tuple(synth.window_partition(x, f, lat_h, lat_w).to(torch.bfloat16).contiguous()
                           for x in (q, k, v)))
-    ring = fvsr_lcsa.KVRing(args.layers, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
+    if smooth:
+        del field
+    ring = fvsr_lcsa.KVRing(layers, H, bh, bw, capacity=4, kv_len=3, dtype=torch.bfloat16)
     outs = [torch.empty_like(d[0]) for d in data]
     qwork = [torch.empty_like(d[0]) for d in data]
 
@@ -282,15 +313,14 @@ def stream_bench(args):
         for c in range(len(chunks)):
             if events is not None:
                 events[c][0].record()
-            for layer in range(args.layers):
+            for layer in range(layers):
                 call(layer, c)
             if events is not None:
                 events[c][1].record()
 
-    for _ in range(max(1, warmup_of(args, 20) // 5)):
+    for _ in range(warm_runs):
         run_stream()
     torch.cuda.synchronize()
-    reps = max(1, args.steps // 10)
     tot = [0.0] * len(chunks)
     for _ in range(reps):
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in chunks]
@@ -298,14 +328,70 @@ def stream_bench(args):
         torch.cuda.synchronize()
         for c, (a0, a1) in enumerate(ev):
             tot[c] += a0.elapsed_time(a1) / reps
-    flops = [4.0 * 128 ** 3 * p * args.layers for p in kept_pairs]
+    flops = [4.0 * 128 ** 3 * p * layers for p in kept_pairs]
     steady = tot[1:]
+    out = {
+        "chunk_ms": [round(t, 3) for t in tot],
+        "per_layer_call_ms": [round(t / layers, 4) for t in tot],
+        "steady_ms_per_layer_call": round(sum(steady) / len(steady) / layers, 4),
+        "chunk0_ms_per_layer_call": round(tot[0] / layers, 4),
+        "kept_block_fraction": [round(p / (H * n * s * min(n + (3 if c else 0), 4) * s), 4)
+                                for c, ((n, _), p) in enumerate(zip(chunks, kept_pairs))],
+        "effective_tflops_kept": [round(f / (t * 1e-3) / 1e12, 1) for f, t in zip(flops, tot)],
+        "steady_ms_per_chunk": round(sum(steady) / len(steady), 3),
+        "topk": topk, "layers": layers, "reps": reps,
+        "_meta": {"H": H, "s": s, "chunks": chunks, "smooth": smooth, "proj": proj},
+    }
+    if split:
+        # one steady layer call taken apart on the last layer's ring (3 slices held): the new slice appended, then
+        # the selection and the attention timed back to back, n calls each; then the slice is evicted again
+        layer, c = layers - 1, len(chunks) - 1
+        (n, t0), (q, k, v) = chunks[c], data[c]
+        qw = qwork[c]
+        if proj:
+            ring.append_qkv(layer, q, k, v, n, t0, wq, wk, q_out=qw)
+        else:
+            qw = q
+            ring.append(layer, k, v, n)
+        _, _, kidx, kcnt = ring.select(layer, qw, n, local, topk, want_mask=False, want_probs=False)
+        o = outs[c]
+        nrep = 20
+        for _ in range(3):
+            ring.select(layer, qw, n, local, topk, want_mask=False, want_probs=False)
+            ring.attention(layer, qw, kidx, kcnt, out=o)
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        for _ in range(nrep):
+            ring.select(layer, qw, n, local, topk, want_mask=False, want_probs=False)
+        e[1].record()
+        for _ in range(nrep):
+            ring.attention(layer, qw, kidx, kcnt, out=o)
+        e[2].record()
+        torch.cuda.synchronize()
+        ring.evict(layer)
+        out["steady_selection_ms"] = round(e[0].elapsed_time(e[1]) / nrep, 4)
+        out["steady_attention_ms"] = round(e[1].elapsed_time(e[2]) / nrep, 4)
+        steady_flops = 4.0 * 128 ** 3 * kept_pairs[c]
+        out["steady_attention_tflops"] = round(steady_flops / (out["steady_attention_ms"] * 1e-3) / 1e12, 1)
+    ring.close()
+    return out
+
+
+def stream_bench(args):
+    """`--stream`: the streaming attention stack on its own JSON line (see stream_measure)."""
+    proj = args.from_projections
+    smooth = not args.iid
+    r = stream_measure(args.layers, max(1, args.steps // 10), max(1, warmup_of(args, 20) // 5), args.seed or 0,
+                       args.iid, proj, split=True)
+    meta = r.pop("_meta")
+    H, s, chunks = meta["H"], meta["s"], meta["chunks"]
     line = {
         "metric": ("LCSA attention stack per streaming chunk, 1920x1152 (q/k/v projections -> norm + RoPE + window "
                    "partition + append + select + attention + evict + window reverse)" if proj else
                    "LCSA attention stack per streaming chunk, 1920x1152 (append + select + attention + evict)"),
         "unit": "ms per chunk (all layers)",
-        "value": round(sum(steady) / len(steady), 3),
+        "value": r["steady_ms_per_chunk"],
         "higher_is_better": False,
         "n_gpus": 1,
         "dtype": "bf16",
@@ -313,16 +399,11 @@ def stream_bench(args):
                  ("; WanRMSNorm weights " + ("~2" if smooth else "~1") if proj else "; per-head RMS norm") +
                  " + 3-D RoPE; no checkpoint"),
         "config": {"workload": "stream_1920x1152_bf16" + ("_from_projections" if proj else "") + ("_iid" if not smooth else ""), "layers": args.layers, "heads": H, "head_dim": 128,
-                   "spatial_blocks_per_slice": s, "local_range": 11, "topk": topk, "kv_window_slices": 3,
+                   "spatial_blocks_per_slice": s, "local_range": 11, "topk": r["topk"], "kv_window_slices": 3,
                    "chunks": [{"query_blocks": n * s, "key_blocks": min(n + (3 if c else 0), 4) * s}
                               for c, (n, _) in enumerate(chunks)]},
-        "chunk_ms": [round(t, 3) for t in tot],
-        "per_layer_call_ms": [round(t / args.layers, 4) for t in tot],
-        "kept_block_fraction": [round(p / (H * n * s * min(n + (3 if c else 0), 4) * s), 4)
-                                for c, ((n, _), p) in enumerate(zip(chunks, kept_pairs))],
-        "effective_tflops_kept": [round(f / (t * 1e-3) / 1e12, 1) for f, t in zip(flops, tot)],
-        "reps": reps,
     }
+    line.update(r)
     print(json.dumps(line), flush=True)
 
 
@@ -614,9 +695,18 @@ def main():
     for _ in range(args.steps):
         select()
     s1.record(stream)
+    # the layer call timed once more, after the two loops above: the first loop runs while the part's clock is still
+    # rising from idle (it settles over roughly 0.1 s of load), this one on a settled clock; `value` stays the first
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record(stream)
+    for _ in range(args.steps):
+        _, _, ki, kc = select()
+        attend(ki, kc)
+    r1.record(stream)
     torch.cuda.synchronize()
     ms_attn = a0.elapsed_time(a1) / args.steps
     ms_select = s0.elapsed_time(s1) / args.steps
+    ms_again = r0.elapsed_time(r1) / args.steps
 
     def timed(fn, n):
         for _ in range(2):
@@ -642,6 +732,9 @@ def main():
     # that select nothing are written as zeros without a walk); includes the mask -> list build (a few us)
     ms_masked = timed(lambda: fvsr_lcsa.block_masked_attention(q, k, v, mask, wl.heads, out=od), nd)
     dense_flops = 4.0 * 128 * wl.heads * wl.lq * wl.lk
+    cpu_inputs = None
+    if not args.no_cpu and not args.no_stream and wl.name == HEADLINE:
+        cpu_inputs = tuple(t.cpu() for t in (q, k, v, mask))
 
     achieved = kept / (ms_attn * 1e-3) / 1e12
     value = kept / (ms_step * 1e-3) / 1e12
@@ -677,6 +770,8 @@ def main():
             "layer_call": round(ms_step, 4),
             "attention_kernel": round(ms_attn, 4),
             "selection": round(ms_select, 4),
+            "selection_plus_attention": round(ms_select + ms_attn, 4),
+            "layer_call_timed_again": round(ms_again, 4),
             "dense_fallback_all_blocks": round(ms_dense, 4),
             "dense_masked_walk": round(ms_masked, 4),
         },
@@ -699,6 +794,25 @@ def main():
         },
         "host_wall_s": round(wall, 3),
     }
+    if not args.no_stream and wl.name == HEADLINE:
+        # the streaming stack of the same resolution (30 layers, chunks of 3, 1, 1, 1, 1 slices from the q/k/v
+        # projections: epilogue + append + select + attention + evict per layer call), one timed pass
+        del q, k, v, o, od, mask, kidx, kcnt
+        torch.cuda.empty_cache()
+        r = stream_measure(30, 1, 1, 0, iid=False, proj=True, split=True)
+        r.pop("_meta")
+        line["stream_1920x1152"] = {
+            "workload": "stream_1920x1152_bf16_from_projections",
+            "steady_ms_per_layer_call": r["steady_ms_per_layer_call"],
+            "chunk0_ms_per_layer_call": r["chunk0_ms_per_layer_call"],
+            "steady_selection_ms": r["steady_selection_ms"],
+            "steady_attention_ms": r["steady_attention_ms"],
+            "steady_attention_tflops": r["steady_attention_tflops"],
+            "chunk_ms_30_layers": r["chunk_ms"],
+            "kept_block_fraction": r["kept_block_fraction"],
+        }
+        if cpu_inputs is not None:
+            q, k, v, mask = cpu_inputs
     if not args.no_cpu and not args.attn_only:
         line["cpu_baseline"] = cpu_baseline(wl, q, k, v, mask, kept, args.cpu_seconds)
     print(json.dumps(line), flush=True)

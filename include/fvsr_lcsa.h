@@ -110,9 +110,11 @@ int fvsr_lcsa_attention(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, con
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and results as
  * fvsr_lcsa_attention; the persistent walk's row order and work counter live in a static device array of the
  * library (1 MiB + 256 B per GPU, held until the process ends) instead of the context workspace, so the call
- * allocates nothing. heads * ceil(lq / 128) must be <= 262144 (FVSR_ERR_UNSUPPORTED otherwise, before any device
- * work). The context must exist (fvsr_ctx_create takes the array's device address). Calls that overlap on one GPU
- * share the array and race: serialise them (one stream, or events). */
+ * allocates nothing. For bf16, heads * ceil(lq / 128) must be <= 262144 (FVSR_ERR_UNSUPPORTED otherwise, before any
+ * device work); the fp32 kernel keeps no row order, so fp32 calls have no such cap. The context must exist
+ * (fvsr_ctx_create takes the array's device address). Calls that overlap on one GPU share the array and race:
+ * serialise them (one stream, or events). The call may be captured into a HIP graph: the order kernel rewrites the
+ * row order and the work counter on every launch, so each replay starts from a clean scratch. */
 int fvsr_lcsa_attention_noalloc(fvsr_ctx* ctx, int dtype, const void* q, int64_t lq, const void* k, const void* v,
                                 int64_t lk, int heads, const int32_t* kidx, const int32_t* kcnt, int nk_stride,
                                 void* o, void* stream);
@@ -199,9 +201,12 @@ int fvsr_lcsa_layer_qkv(fvsr_ctx* ctx, fvsr_kv_ring* ring, int layer, const void
 
 /* ---- (f3) the dense parts of the DiT block ------------------------------------------------------------------ */
 /* No reference counterpart (MLX allocates lazily): make the DiT-block entry points allocation-free for blocks of up to
- * `tokens` tokens (heads * 128 channels, FFN width ffn_dim, ctx_len context tokens) over a ring window of up to
- * `key_tokens` keys. Creates the context's hipBLASLt handle and 64 MB GEMM workspace, grows the block workspace
- * (about (8 C + F) * tokens * 2 bytes) and the select/attention workspace. */
+ * `tokens` tokens (heads * 128 channels, FFN width ffn_dim, ctx_len context tokens) whose attention sees up to
+ * `key_tokens` keys. A layer call attends over the held slices plus the chunk's new ones before the trim, so
+ * key_tokens must cover min(capacity, kv_len + largest n_new_slices) * s * 128 (not kv_len slices alone: a call
+ * past the reserved size grows the workspace, and that hipFree synchronises the device). Creates the context's
+ * hipBLASLt handle and 64 MB GEMM workspace, grows the block workspace (about (8 C + F) * tokens * 2 bytes) and the
+ * select/attention workspace. */
 int fvsr_ctx_reserve_block(fvsr_ctx* ctx, int heads, int64_t tokens, int ffn_dim, int ctx_len, int64_t key_tokens);
 size_t fvsr_ctx_block_workspace_bytes(const fvsr_ctx* ctx);
 

@@ -20,8 +20,8 @@ PROBE = os.path.join(LIB_DIR, "fvsr_probe_attn")
 
 SOURCES = ["api.hip", "lcsa_attn.hip", "lcsa_select.hip", "kv_ring.hip", "qkv_epilogue.hip", "dit_block.hip"]
 # Packed-FP32 VALU forms are disabled: hipcc -O3 would otherwise emit v_pk_{add,mul,fma}_f32 from float code.
-# MFMA builtins get the VGPR form (results in VGPRs, where the VALU reads them without v_accvgpr_read); the attention
-# kernels write the one AGPR-accumulating MFMA as inline assembly.
+# MFMA builtins get the VGPR form (results in VGPRs, where the VALU reads them without v_accvgpr_read); every MFMA
+# of the attention kernels, the output accumulation included, is a compiler builtin.
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature", "-Xclang",
              "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form"]
 

@@ -362,7 +362,10 @@ int fvsr_lcsa_attention_noalloc(fvsr_ctx* ctx, int dtype, const void* q, int64_t
   FVSR_REQUIRE(nk_stride > 0, FVSR_ERR_INVALID_ARG, "nk_stride must be > 0");
   const int nk = (int)ceil_div(lk, kBlock);
   AttnArgs a = make_args(q, lq, k, v, lk, heads, kidx, kcnt, nullptr, nk_stride, nk, plain_key_map(), o, esize(dtype));
-  if ((rc = noalloc_scratch(ctx->device, (int64_t)heads * a.nq, &a.order, &a.counter))) return rc;
+  // only the bf16 walk keeps a row order and a work counter; the fp32 kernel has neither, so no row cap applies
+  if (dtype == FVSR_DTYPE_BF16 &&
+      (rc = noalloc_scratch(ctx->device, (int64_t)heads * a.nq, &a.order, &a.counter)))
+    return rc;
   FVSR_HIP_CHECK(hipSetDevice(ctx->device));
   return launch_attention(dtype, false, a, (hipStream_t)stream);
 }

@@ -217,7 +217,7 @@ def test_c2_full_mask_sparse_equals_dense_bf16(dev):
 
 def _rows_vs_oracle(q, k, v, mask_np, heads, o, pairs):
     """Worst rel of the GPU output against the float64 oracle over the listed (head, query block) rows."""
-    qn, kn, vn = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    qn, kn, vn = q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy()
     got = _np(o)
     worst = 0.0
     for h, b in pairs:
@@ -226,6 +226,22 @@ def _rows_vs_oracle(q, k, v, mask_np, heads, o, pairs):
         c = slice(h * 128, (h + 1) * 128)
         worst = max(worst, O.compare(got[r, c], ref[r, c])["rel"])
     return worst
+
+
+def test_c2_full_mask_every_head_vs_oracle(dev):
+    """1280x768 bf16, every block kept (DiT.swift:279-313 with a full mask): three query blocks of EVERY head (the
+    first, a middle and the last of the 60) against the float64 oracle at rel <= 1e-2, for the sparse kernel and
+    for the dense fallback; the two are equal bit for bit."""
+    wl = synth.WORKLOADS["dense_1280x768_bf16"]
+    q, k, v = synth.make_qkv(wl, seed=0, device=dev)
+    m = torch.ones((wl.heads, wl.nq, wl.nk), device=dev)
+    o = fvsr_lcsa.kernel_block_attention(q, k, v, m, wl.heads)
+    od = fvsr_lcsa.block_masked_attention(q, k, v, m, wl.heads)
+    assert torch.equal(o, od)
+    mask_np = np.ones((wl.heads, wl.nq, wl.nk), dtype=np.float32)
+    pairs = [(h, b) for h in range(wl.heads) for b in (0, (7 * h + 23) % wl.nq, wl.nq - 1)]
+    rel = _rows_vs_oracle(q, k, v, mask_np, wl.heads, o, pairs)
+    assert rel <= BF16_REL, rel
 
 
 def test_c4_bf16_subset_vs_oracle(dev):

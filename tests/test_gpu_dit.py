@@ -151,7 +151,9 @@ def test_reserved_block_calls_allocate_nothing(dev):
     ring = fvsr_lcsa.KVRing(1, heads, bh, bw, capacity=4, kv_len=3, device=dev.index or 0)
     fresh = fvsr_lcsa.Context(dev.index or 0)      # a context no earlier call has grown
     ring.ctx = fresh
-    tokens, key_tokens = 2 * s * 128, 4 * s * 128   # the largest chunk (2 slices) over the fullest window (4 slices)
+    # the largest chunk (2 slices) over the fullest window: kv_len 3 held + 1 new = 4 slices = the capacity, exactly
+    # what the header asks for (min(capacity, kv_len + largest chunk) slices); the last call below attends over it
+    tokens, key_tokens = 2 * s * 128, 4 * s * 128
     fresh.reserve_block(heads, tokens, ffn, ctx_len, key_tokens)
     ws, bws = fresh.workspace_bytes(), fresh.block_workspace_bytes()
     assert ws > 0 and bws > 0

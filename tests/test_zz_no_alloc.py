@@ -80,3 +80,41 @@ def test_noalloc_refuses_rows_beyond_its_scratch(dev):
                                               None)
     assert rc == _abi.ERR_UNSUPPORTED
     assert b"static scratch" in _abi.lib.fvsr_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_replays_under_graph_capture(dev, dtype):
+    """The allocation-free call captured into a HIP graph (torch.cuda.CUDAGraph) and replayed three times with new
+    q/k/v and new key lists copied into the captured buffers, eager work in between: every replay equals
+    fvsr_lcsa_attention on the same inputs bit for bit (the order kernel rewrites the scratch's row order and work
+    counter on each replay)."""
+    ctx = _fresh_ctx(dev)
+    try:
+        heads, lqb, lk = 6, 20, 12 * 128 + 64
+        q, k, v, kidx, kcnt, _, _ = _case(dev, dtype, heads, lqb, lk, 10)
+        o_graph = torch.zeros_like(q)
+        o_ws = torch.zeros_like(q)
+        _attend("fvsr_lcsa_attention_noalloc", ctx, q, k, v, kidx, kcnt, heads, o_graph)   # eager first call
+        torch.cuda.synchronize()
+        ws = _abi.lib.fvsr_ctx_workspace_bytes(ctx)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            _attend("fvsr_lcsa_attention_noalloc", ctx, q, k, v, kidx, kcnt, heads, o_graph)
+        assert _abi.lib.fvsr_ctx_workspace_bytes(ctx) == ws
+        for rep, seed in enumerate((11, 12, 13)):
+            print(f"  graph replay {rep} {dtype} seed {seed}", flush=True)
+            q2, k2, v2, kidx2, kcnt2, _, _ = _case(dev, dtype, heads, lqb, lk, seed)
+            for dst, src in ((q, q2), (k, k2), (v, v2), (kidx, kidx2), (kcnt, kcnt2)):
+                dst.copy_(src)
+            o_graph.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            _attend("fvsr_lcsa_attention", ctx, q, k, v, kidx, kcnt, heads, o_ws)      # eager, between replays
+            torch.cuda.synchronize()
+            assert not torch.isnan(o_graph).any()
+            assert torch.equal(o_graph, o_ws), rep
+        del g
+    finally:
+        torch.cuda.synchronize()
+        _abi.lib.fvsr_ctx_destroy(ctx)
