@@ -435,8 +435,8 @@ struct RowStream {
   }
 };
 
-// probs: (H, nq, nk); hist: (H * q_slices, kHistBins) from scores_softmax_kernel. Grid: (ceil(sq / kEmitRows),
-// H * q_slices).
+// probs: (H, nq, nk); hist: (H * q_slices, kHistBins) from scores_softmax_kernel. Grid: ceil(sq / kEmitRows) *
+// H * q_slices workgroups.
 __global__ __launch_bounds__(kEmitThreads) void topk_emit_kernel(const float* __restrict__ probs,
                                                                  const unsigned* __restrict__ hist12, int nq, int nk,
                                                                  int q_slices, int topk,
@@ -457,11 +457,16 @@ __global__ __launch_bounds__(kEmitThreads) void topk_emit_kernel(const float* __
   __shared__ unsigned wsum[NT / 64];
   __shared__ unsigned s_prefix, s_rank, s_ncand, s_nc;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int row = blockIdx.y;                    // (head, query slice)
-  const int h = row / q_slices, t = row % q_slices;
+  // (head, query slice) row and group from the XCD-remapped workgroup index, row-major: a row's workgroups share
+  // one XCD (and, rows being head-major like the scores kernel's workgroups, the XCD whose L2 the row's probs were
+  // written through), so its L2 serves the row to all of them
   const int sq = nq / q_slices;
-  const int qi = t * sq + blockIdx.x * kEmitRows + wave;   // this wave's query block
-  const bool has_row = blockIdx.x * kEmitRows + wave < sq;  // wave-uniform
+  const int gx = (sq + kEmitRows - 1) / kEmitRows;   // workgroups per row
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
+  const int row = lid / gx, grp = lid - row * gx;
+  const int h = row / q_slices, t = row % q_slices;
+  const int qi = t * sq + grp * kEmitRows + wave;   // this wave's query block
+  const bool has_row = grp * kEmitRows + wave < sq;  // wave-uniform
   const unsigned* __restrict__ bits = (const unsigned*)(probs + ((int64_t)h * nq + (int64_t)t * sq) * nk);
   const int n = sq * nk;                           // < 2^31 (the host checks)
   const int k = min(n - 1, topk);
@@ -469,7 +474,7 @@ __global__ __launch_bounds__(kEmitThreads) void topk_emit_kernel(const float* __
   const RowStream<NT> rs(bits, n);
   // this workgroup's query blocks are elements [own0, own0 + own_n) of the row
   const bool stage_own = nk <= kEmitOwnMax;
-  const int own0 = blockIdx.x * kEmitRows * nk;
+  const int own0 = grp * kEmitRows * nk;
   const int own_n = stage_own ? min(kEmitRows * nk, n - own0) : 0;
 
   // first loads, all issued before the first wait: the histogram (thread tid owns bins kBinsPer * tid ..), the row's
@@ -715,7 +720,7 @@ int launch_topk_emit(const float* probs, const unsigned* hist, int heads, int nq
   const int sq = nq / q_slices;
   if ((int64_t)sq * nk >= ((int64_t)1 << 31))
     return set_error(FVSR_ERR_UNSUPPORTED, "selection: a (head, query slice) row of 2^31 or more block pairs");
-  hipLaunchKernelGGL(topk_emit_kernel, dim3((unsigned)ceil_div(sq, kEmitRows), (unsigned)(heads * q_slices)),
+  hipLaunchKernelGGL(topk_emit_kernel, dim3((unsigned)(ceil_div(sq, kEmitRows) * heads * q_slices)),
                      dim3(kEmitThreads), 0, stream, probs, hist, nq, nk, q_slices, topk, mask_out, sel, kidx, kcnt);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
