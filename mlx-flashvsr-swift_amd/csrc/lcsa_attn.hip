@@ -479,7 +479,7 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
     // step with tile T in ring slot SUB: K(T+4) -> slot SUB, V(T+2) -> slot SUB+2, QK(T+1) <- K slot SUB+1,
     // PV(T-1) <- V slot SUB+3 (all mod 4)
     auto step = [&](auto sub_c, int valid_next, int soff_k, int soff_v, f32x16 (&s_cur)[QG], f32x16 (&s_nxt)[QG],
-                    bf16x8 (&p_prev)[QG][2], bf16x8 (&p_cur)[QG][2]) {
+                    bf16x8 (&p_prev)[QG][2], bf16x8 (&p_cur)[QG][2], auto&& pre_sync) {
       constexpr int SUB = decltype(sub_c)::value;
       using KS = std::integral_constant<int, SUB>;
       using VS = std::integral_constant<int, (SUB + 2) & 3>;
@@ -561,6 +561,10 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
             if constexpr ((J & 1) == 1) {
               p_cur[qj][ij >> 3][(ij & 7) - 1] = (bf16)xv[0];
               p_cur[qj][ij >> 3][ij & 7] = (bf16)xv[1];
+              // the pair is packed here, in this micro-round: without a use before the reference check the
+              // compiler sinks the packs past it (the raise recomputes them) into the step's tail
+              const u32x4 pw = __builtin_bit_cast(u32x4, p_cur[qj][ij >> 3]);
+              asm volatile("" ::"v"(pw[(ij & 7) >> 1]));
             }
           }
           if constexpr (I < 16 * QG) {
@@ -622,17 +626,20 @@ void attn_bf16_kernel(AttnArgs a, const int32_t* __restrict__ kidx, const int32_
       // keep every instruction of this step on its side of the barrier; the copies of the step before have landed
       // (the next step's first operands, read above, were waited for one step earlier)
       __builtin_amdgcn_sched_barrier(0);
+      pre_sync();
       sync_steps(1);
       __builtin_amdgcn_sched_barrier(0);
     };
     for (int b = 0; b < nblocks; ++b) {
       const int o3 = entry_soff(b + 3, e3), n3 = entry_keys(b + 3, e3);
-      e3 = walk_entry(b + 4);
       // step 4b+s: QK tile 4b+s+1, K tile 4b+s+4 (block b+1), V tile 4b+s+2
-      step(C0{}, sub_valid(n0, 1), o1, o0 + 2 * sub_bytes, sA, sB, pB, pA);
-      step(C1{}, sub_valid(n0, 2), o1 + sub_bytes, o0 + 3 * sub_bytes, sB, sA, pA, pB);
-      step(C2{}, sub_valid(n0, 3), o1 + 2 * sub_bytes, o1, sA, sB, pB, pA);
-      step(C3{}, sub_valid(n1, 0), o1 + 3 * sub_bytes, o1 + sub_bytes, sB, sA, pA, pB);
+      auto nop = [] {};
+      step(C0{}, sub_valid(n0, 1), o1, o0 + 2 * sub_bytes, sA, sB, pB, pA, nop);
+      step(C1{}, sub_valid(n0, 2), o1 + sub_bytes, o0 + 3 * sub_bytes, sB, sA, pA, pB, nop);
+      step(C2{}, sub_valid(n0, 3), o1 + 2 * sub_bytes, o1, sA, sB, pB, pA, nop);
+      // the next block's list entry loads right before the step's wait, which absorbs it
+      step(C3{}, sub_valid(n1, 0), o1 + 3 * sub_bytes, o1 + sub_bytes, sB, sA, pA, pB,
+           [&] { e3 = walk_entry(b + 4); });
       o0 = o1; o1 = o2; o2 = o3;
       n0 = n1; n1 = n2; n2 = n3;
     }
