@@ -30,8 +30,9 @@ int launch_sel_from_lists(const int32_t* kidx, const int32_t* kcnt, int rows, in
 int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int heads, int C, int nq, int nk, int s,
                           const uint8_t* local, float* probs, unsigned* hist, int q_slices, hipStream_t stream);
 size_t hist12_bytes(int heads, int q_slices);
-int launch_topk_emit(const float* probs, const unsigned* hist, int heads, int nq, int nk, int q_slices, int topk,
-                     float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt,
+size_t topk_cand_bytes(int heads, int64_t nq);
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, unsigned* hist,
+                     unsigned* cand, float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt,
                      hipStream_t stream);
 int launch_qkv_epilogue(int dtype, const void* q, const void* k, const void* v, int f, int h, int w, int C, int t0,
                         const void* wq, const void* wk, float eps, const float* rope, void* q_out, void* k_out,
@@ -67,7 +68,7 @@ static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // workspace carve for one select + attention call
 struct Carve {
-  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, hist, total;
+  size_t pq, pk, probs, kidx, kcnt, sel, order, counter, thr, hist, cand, total;
 };
 static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   Carve c;
@@ -80,7 +81,9 @@ static Carve carve(int heads, int64_t nq, int64_t nk, int C) {
   c.sel = off; off += align256((size_t)heads * nq * nk);
   c.order = off; off += align256((size_t)heads * nq * 4);
   c.counter = off; off += 256;
+  c.thr = off; off += align256((size_t)heads * nq * 4);   // per (head, query slice) thresholds (nq >= slices)
   c.hist = off; off += align256(hist12_bytes(heads, (int)nq));   // nq >= query slices
+  c.cand = off; off += align256(topk_cand_bytes(heads, nq));
   c.total = off;
   return c;
 }
@@ -267,7 +270,8 @@ static int select_impl(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, con
   }
   if ((rc = launch_scores_softmax(pq, pk, kmap, heads, C, (int)nq, nk, s, local, probs, hist, q_slices, stream)))
     return rc;
-  return launch_topk_emit(probs, hist, heads, (int)nq, nk, q_slices, topk, mask_out, sel, kidx, kcnt, stream);
+  return launch_topk_emit(probs, heads, (int)nq, nk, q_slices, topk, hist, (unsigned*)(ws + cv.cand),
+                          (float*)(ws + cv.thr), mask_out, sel, kidx, kcnt, stream);
 }
 
 int fvsr_lcsa_select(fvsr_ctx* ctx, int dtype, const void* qW, int64_t lq, const void* kW, int64_t lk, int heads,

@@ -18,12 +18,13 @@
 //                         coalesced chunks of 64 keys, two chunks side by side, read once per 8 query rows; scores
 //                         + local mask in LDS, one wave per row for max / exp / sum / normalise; it also counts the
 //                         nonzero probs of each (head, query slice) per top-12-bit bin
-//   topk_emit_kernel     one 16-wave workgroup per 16 query blocks of a (head, query slice) row: each finds the
-//                        row's exact (k+1)-th largest by itself (the histogram picks the bin, the row is streamed
-//                        once to gather that bin's elements into LDS, two radix digits finish the low 19 bits;
-//                        full-row 4-pass radix select when the bin is too large), then each wave emits one query
-//                        block: mask, selection bytes and compacted key lists (ballot + popcount), from its row of
-//                        probs staged in LDS
+//   topk_threshold_kernel 16 workgroups of 256 threads per (head, query slice): exact (k+1)-th largest over the
+//                         fp32 bit patterns (probs are >= 0, so bit order = value order): the histogram picks the
+//                         bin, each workgroup gathers the bin's elements of its share of the row (held in
+//                         registers), and the last to arrive finishes the low 19 bits by three radix passes in LDS
+//                         (full-row 4-pass radix select when the bin is too large)
+//   topk_emit_kernel     one wave per query row: mask, selection bytes and compacted key lists (ballot + popcount),
+//                        the row's probs loaded into registers at once
 #include "common.hpp"
 
 namespace fvsr {
@@ -309,55 +310,52 @@ __global__ __launch_bounds__(kScoreThreads) void scores_softmax_kernel(const flo
 // ------------------------------------------------------------------------------------------------------------
 // exact top-k threshold + mask / list emit
 // ------------------------------------------------------------------------------------------------------------
-// One workgroup of kEmitRows waves per kEmitRows query blocks of one (head, query slice) row of n = sq * Nk probs.
-// Each workgroup finds that row's (k+1)-th largest, k = min(n - 1, topk), by itself, by an exact select over the fp32
-// bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0): the row's top-12-bit histogram (built
-// by scores_softmax_kernel) gives the bin that holds the threshold and its rank in the bin; the row is streamed once
-// (its first loads issued with the histogram's, before the bin is known) and the elements of that bin are gathered
-// into LDS; two radix digits over them, [18:9] and [8:0], each a workgroup histogram in LDS, resolve the remaining
-// 19 bits. A bin too large for LDS (the threshold on the exact zeros outside the local window) makes it run a
-// full-row radix select from memory instead: exponent [30:23], then mantissa [22:15], [14:7], [6:0], with the zeros
-// counted by a wave ballot instead of 64 colliding LDS atomics. The workgroups of a row repeat the same select on
-// the same data (after the first, from L2): none waits for another and nothing moves between them, so no memory
-// ordering between workgroups is involved. Then wave w emits query block w of the workgroup: mask, selection bytes
-// and the key list (selected key blocks ascending, then the unselected ascending: argSort(!sel) of
-// SparseAttention.swift:177 with a stable order), from its row of probs, which the workgroup loads with its first
-// loads and stages in LDS.
-// (Against a select shared by 16 workgroups per row through a candidate area and an arrival count, then a separate
-// emit launch: equal time on the 135 x 338 rows of the 1920x1152 workload, 20-25 us less on the streaming 135 x 540
-// rows, where that select took 13.9 us and its emit 6.5.)
-constexpr int kEmitRows = 16;                // query blocks (waves) per workgroup
-constexpr int kEmitThreads = 64 * kEmitRows;
-constexpr int kEmitOwnMax = 768;              // key blocks per query block staged in LDS for the emit (longer rows
-                                              // are read again from memory)
-constexpr int kScanVec = 12;                  // 16-byte loads per thread in flight while a row streams
-constexpr int kSelCand = 8192;                // candidates held in LDS
+// The (k+1)-th largest of each (head, query slice) row of s*Nk probs, k = min(n-1, topk), by an exact select over
+// the fp32 bit patterns (probs are >= 0, so bit order = value order and bit 31 is 0). kThrParts or more workgroups
+// share a row. Each reads the row's top-12-bit histogram (built by scores_softmax_kernel), finds the bin that holds the
+// threshold and its rank in the bin (all of them find the same), then scans its share of the row and gathers the
+// elements of that bin into the row's candidate area of the workspace. The candidates and the arrival count move
+// as relaxed agent-scope atomics (coherent stores and loads past this XCD's L2), ordered by the wait for the stores
+// and the barrier before the arrival add; the workgroup that arrives last loads the candidates into LDS and
+// resolves the remaining 19 bits by three radix passes (digits [18:11], [10:3], [2:0]). A bin too large for the
+// candidate area (e.g. the threshold falls on the exact zeros outside the local window) makes that last workgroup
+// run a full-row radix select from memory instead: exponent [30:23], then mantissa [22:15], [14:7], [6:0], with the
+// zeros counted by a wave ballot instead of 64 colliding LDS atomics.
+constexpr int kThrParts = 16;           // workgroups per (head, query slice) row, at least (more for long rows)
+constexpr int kThrMaxParts = 64;
+constexpr int kThrThreads = 256;
+constexpr int kThrLdsCand = 16384;      // candidates the last workgroup holds in LDS
+constexpr int kCandPerBlock = 128;      // candidate words of the workspace per (head, query block)
+constexpr int kThrRegs = 16;            // elements per thread held in registers (a share of up to 4096)
 
-// One radix digit over the elements `visit` presents, in a workgroup of NT threads: every element matching `prefix`
-// under `pmask` is histogrammed by its digit (u >> shift) & dmask; the digit holding ascending rank `rank` extends
-// `prefix`, and `rank` becomes the rank inside it. Zeros matching the prefix are counted by ballot (they all fall in
-// digit 0). hist: NT / 64 x 256 words, tot: 256 words (LDS).
-template <int NT, class Visit>
-__device__ __forceinline__ void radix_digit(unsigned* hist, unsigned* tot, unsigned& prefix, unsigned& rank,
-                                            unsigned pmask, int shift, unsigned dmask, Visit&& visit,
-                                            unsigned* s_prefix, unsigned* s_rank) {
+// per-row control words after the histograms: [0] candidates gathered, [1] workgroups arrived
+__device__ __forceinline__ unsigned* thr_ctl(unsigned* hist12, int rows, int row) {
+  return hist12 + (int64_t)rows * kHistBins + 2 * row;
+}
+
+// One radix digit over `count(visit)` of a workgroup of kThrThreads: every (masked) element visited is histogrammed
+// by its digit (u >> shift) & dmask; the digit holding ascending rank `rank` extends `prefix`, `rank` becomes the
+// rank inside it. Zeros matching the prefix are counted by ballot (they all fall in digit 0).
+template <class Visit>
+__device__ __forceinline__ void radix_digit(unsigned (&hist)[kThrThreads / 64][256], unsigned* tot,
+                                            unsigned& prefix, unsigned& rank, unsigned pmask, int shift,
+                                            unsigned dmask, Visit&& visit, unsigned* s_prefix, unsigned* s_rank) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  for (int e = tid; e < (NT / 64) * 256; e += NT) hist[e] = 0;
+  for (int e = tid; e < (kThrThreads / 64) * 256; e += kThrThreads) (&hist[0][0])[e] = 0;
   __syncthreads();
   unsigned zeros = 0;
-  unsigned* const wh = hist + wave * 256;
-  visit([&](unsigned u, int) {   // called by every lane of the wave together
+  visit([&](unsigned u) {   // called by every lane of the wave together
     const bool match = (u & pmask) == prefix;
     const bool z = match && u == 0u;
     zeros += __popcll(__ballot(z));
-    wave_hist_add(wh, (u >> shift) & dmask, match && !z);
+    wave_hist_add(hist[wave], (u >> shift) & dmask, match && !z);
   });
-  if (lane == 0 && zeros) atomicAdd(&wh[0], zeros);
+  if (lane == 0 && zeros) atomicAdd(&hist[wave][0], zeros);
   __syncthreads();
-  if (tid < 256) {
+  {
     unsigned c = 0;
 #pragma unroll
-    for (int w = 0; w < NT / 64; ++w) c += hist[w * 256 + tid];
+    for (int w = 0; w < kThrThreads / 64; ++w) c += hist[w][tid];
     tot[tid] = c;
   }
   __syncthreads();
@@ -386,143 +384,75 @@ __device__ __forceinline__ void radix_digit(unsigned* hist, unsigned* tot, unsig
   rank = *s_rank;
 }
 
-// A row bits[0 .. n) of probability bit patterns as seen by a workgroup of NT threads: the unaligned head and tail
-// (< 4 elements each, 4-byte loads by threads 0..5) and the 16-byte groups between them, kScanVec per thread per pass.
-// Every load is inside the row. f(u, e) sees element e of the row; a slot past it presents u = 0xffffffff (bit 31
-// set: it matches no probability) and e = -1.
-template <int NT>
-struct RowStream {
-  const unsigned* bits;
-  int n, a0, nb, t0;   // n < 2^31 (launch_topk_emit checks)
-  __device__ __forceinline__ RowStream(const unsigned* b, int n_) : bits(b), n(n_) {
-    const int mis = (int)(((uintptr_t)b >> 2) & 3);
-    a0 = min(n, (4 - mis) & 3);      // head: the elements before the first 16-byte boundary
-    nb = (n - a0) >> 2;              // whole 16-byte groups
-    t0 = a0 + 4 * nb;                // tail start
-  }
-  __device__ __forceinline__ int edge_index() const {   // this thread's head or tail element, or -1
-    const int tid = threadIdx.x;
-    if (tid < a0) return tid;
-    if (tid >= 3 && tid - 3 < n - t0) return t0 + tid - 3;
-    return -1;
-  }
-  __device__ __forceinline__ unsigned edge(int e) const { return e >= 0 ? bits[e] : 0xffffffffu; }
-  // groups v0 + tid + NT i, i < kScanVec (clamped: no branch between the loads)
-  __device__ __forceinline__ void load(int v0, u32x4 (&x)[kScanVec]) const {
-    const u32x4* vb = (const u32x4*)(bits + a0);
-#pragma unroll
-    for (int i = 0; i < kScanVec; ++i) x[i] = vb[min(v0 + (int)threadIdx.x + i * NT, nb - 1)];
-  }
-  template <class F>
-  __device__ __forceinline__ void visit(int v0, const u32x4 (&x)[kScanVec], F&& f) const {
-#pragma unroll
-    for (int i = 0; i < kScanVec; ++i) {
-      const int g = v0 + (int)threadIdx.x + i * NT;
-      const bool ok = g < nb;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) f(ok ? x[i][c] : 0xffffffffu, ok ? a0 + 4 * g + c : -1);
-    }
-  }
-  template <class F>
-  __device__ __forceinline__ void each(F&& f) const {   // the whole row from memory
-    const int e = edge_index();
-    f(edge(e), e);
-    for (int v0 = 0; v0 < nb; v0 += NT * kScanVec) {
-      u32x4 x[kScanVec];
-      load(v0, x);
-      visit(v0, x, f);
-    }
-  }
-};
-
-// probs: (H, nq, nk); hist: (H * q_slices, kHistBins) from scores_softmax_kernel. Grid: ceil(sq / kEmitRows) *
-// H * q_slices workgroups.
-__global__ __launch_bounds__(kEmitThreads) void topk_emit_kernel(const float* __restrict__ probs,
-                                                                 const unsigned* __restrict__ hist12, int nq, int nk,
-                                                                 int q_slices, int topk,
-                                                                 float* __restrict__ mask_out,
-                                                                 uint8_t* __restrict__ sel,
-                                                                 int32_t* __restrict__ kidx,
-                                                                 int32_t* __restrict__ kcnt) {
-  constexpr int NT = kEmitThreads;
-  constexpr int kBinsPer = kHistBins / NT;
-  static_assert(kHistBins % NT == 0 && kBinsPer % 4 == 0, "histogram bins per thread, in 16-byte loads");
-  constexpr int kDigitBins = 1024, kDigitPer = kDigitBins / NT;   // candidate-digit bins per thread
-  static_assert(kDigitBins % NT == 0, "candidate-digit bins per thread");
-  __shared__ unsigned cand[kSelCand];
-  __shared__ float own[kEmitRows * kEmitOwnMax];   // this workgroup's query blocks' probs
-  __shared__ unsigned rh[(NT / 64) * 256];          // digit histograms (full-row fallback)
+// per: the elements of a row each workgroup scans, ceil(sq * nk / gridDim.x) (a host-side division: a 64-bit divide
+// here would put branches between the histogram's loads and the share's)
+__global__ __launch_bounds__(kThrThreads) void topk_threshold_kernel(const float* __restrict__ probs, int nq,
+                                                                     int nk, int q_slices, int topk, int64_t per,
+                                                                     unsigned* __restrict__ hist12,
+                                                                     unsigned* __restrict__ cand_ws,
+                                                                     float* __restrict__ thr_out) {
+  static_assert(kThrThreads == 256, "the digit scan gives each thread of a 256-thread workgroup one digit");
+  __shared__ unsigned hist[kThrThreads / 64][256];
   __shared__ unsigned tot[256];
-  __shared__ unsigned dh[kDigitBins];               // digit histogram of the candidates
-  __shared__ unsigned wsum[NT / 64];
-  __shared__ unsigned s_prefix, s_rank, s_ncand, s_nc;
+  __shared__ unsigned wsum[kThrThreads / 64];
+  __shared__ unsigned s_prefix, s_rank, s_ncand, s_arrived;
+  __shared__ unsigned cand[kThrLdsCand];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // (head, query slice) row and group from the XCD-remapped workgroup index, row-major: a row's workgroups share
-  // one XCD (and, rows being head-major like the scores kernel's workgroups, the XCD whose L2 the row's probs were
-  // written through), so its L2 serves the row to all of them
-  const int sq = nq / q_slices;
-  const int gx = (sq + kEmitRows - 1) / kEmitRows;   // workgroups per row
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int row = lid / gx, grp = lid - row * gx;
+  const int part = blockIdx.x, row = blockIdx.y;   // row = (head, query slice)
+  const int rows = gridDim.y;
   const int h = row / q_slices, t = row % q_slices;
-  const int qi = t * sq + grp * kEmitRows + wave;   // this wave's query block
-  const bool has_row = grp * kEmitRows + wave < sq;  // wave-uniform
+  const int sq = nq / q_slices;
   const unsigned* __restrict__ bits = (const unsigned*)(probs + ((int64_t)h * nq + (int64_t)t * sq) * nk);
-  const int n = sq * nk;                           // < 2^31 (the host checks)
-  const int k = min(n - 1, topk);
+  const int64_t n = (int64_t)sq * nk;
+  const int64_t k = min<int64_t>(n - 1, topk);
   const unsigned rank0 = (unsigned)(n - 1 - k);   // ascending rank of the (k+1)-th largest
-  const RowStream<NT> rs(bits, n);
-  // this workgroup's query blocks are elements [own0, own0 + own_n) of the row
-  const bool stage_own = nk <= kEmitOwnMax;
-  const int own0 = grp * kEmitRows * nk;
-  const int own_n = stage_own ? min(kEmitRows * nk, n - own0) : 0;
+  const unsigned cap = (unsigned)min<int64_t>((int64_t)sq * kCandPerBlock, kThrLdsCand);
+  unsigned* const cw = cand_ws + ((int64_t)h * nq + (int64_t)t * sq) * kCandPerBlock;
+  unsigned* const ctl = thr_ctl(hist12, rows, row);
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
-  // first loads, all issued before the first wait: the histogram (thread tid owns bins kBinsPer * tid ..), the row's
-  // first kScanVec groups per thread and its unaligned edges
+  // 1. the threshold's bin from the histogram: thread tid owns bins 16 tid .. 16 tid + 15
   const unsigned* hrow = hist12 + (int64_t)row * kHistBins;
-  unsigned hv[kBinsPer];
+  unsigned hv[16];
 #pragma unroll
-  for (int i = 0; i < kBinsPer; i += 4) {
-    const u32x4 x = *(const u32x4*)(hrow + kBinsPer * tid + i);
-    hv[i] = x[0];
-    hv[i + 1] = x[1];
-    hv[i + 2] = x[2];
-    hv[i + 3] = x[3];
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 x = *(const u32x4*)(hrow + 16 * tid + 4 * i);
+    hv[4 * i] = x[0];
+    hv[4 * i + 1] = x[1];
+    hv[4 * i + 2] = x[2];
+    hv[4 * i + 3] = x[3];
   }
-  u32x4 x0[kScanVec];
-  rs.load(0, x0);
-  const int ei = rs.edge_index();
-  const unsigned e0 = rs.edge(ei);
-  constexpr int kOwnPer = kEmitRows * kEmitOwnMax / NT;   // own-row elements per thread (clamped loads)
-  float ow[kOwnPer];
-  if (stage_own) {
-    const float* ob = probs + ((int64_t)h * nq + (int64_t)t * sq) * nk + own0;
+  // this workgroup's share of the row: up to kThrRegs * kThrThreads elements are loaded into registers here, every
+  // load in flight with the histogram's (they do not depend on the bin; indices are clamped rather than branched
+  // around, so the histogram can be waited for alone), and both counted and gathered from there in step 2; a larger
+  // share is read twice there
+  const int64_t e0 = part * per, e1 = min<int64_t>(n, e0 + per);
+  const bool in_regs = per <= (int64_t)kThrRegs * kThrThreads;
+  unsigned rv[kThrRegs];   // loaded even when unused (a larger share): a branch here would drain the histogram's
+                           // loads and these together
 #pragma unroll
-    for (int i = 0; i < kOwnPer; ++i) ow[i] = ob[min(tid + i * NT, own_n - 1)];
+  for (int i = 0; i < kThrRegs; ++i) {
+    const int64_t e = e0 + tid + (int64_t)i * kThrThreads;
+    rv[i] = bits[min(e, n - 1)];   // entries past the share are masked where they are used (in_share)
   }
-
-  // 1. the threshold's bin from the histogram
   unsigned psum = 0;
 #pragma unroll
-  for (int i = 0; i < kBinsPer; ++i) psum += hv[i];
+  for (int i = 0; i < 16; ++i) psum += hv[i];
   const unsigned incl = wave_incl_scan(psum);
   if (lane == 63) wsum[wave] = incl;
-  if (tid == 0) {
-    s_ncand = 0xffffffffu;
-    s_nc = 0u;
-  }
+  if (tid == 0) s_ncand = 0xffffffffu;
   __syncthreads();
   unsigned wbase = 0, all = 0;
 #pragma unroll
-  for (int w = 0; w < NT / 64; ++w) {
+  for (int w = 0; w < kThrThreads / 64; ++w) {
     wbase += w < wave ? wsum[w] : 0u;
     all += wsum[w];
   }
   const unsigned zeros = (unsigned)n - all;        // the zeros sort first and sit in bin 0
   unsigned cum = wbase + incl - psum + (tid > 0 ? zeros : 0u);
 #pragma unroll
-  for (int i = 0; i < kBinsPer; ++i) {
-    const int bn = kBinsPer * tid + i;
+  for (int i = 0; i < 16; ++i) {
+    const int bn = 16 * tid + i;
     const unsigned c = hv[i] + (bn == 0 ? zeros : 0u);
     if (rank0 >= cum && rank0 < cum + c) {
       s_prefix = (unsigned)bn << 19;
@@ -532,112 +462,137 @@ __global__ __launch_bounds__(kEmitThreads) void topk_emit_kernel(const float* __
     cum += c;
   }
   __syncthreads();
-  unsigned prefix = s_prefix, rk = s_rank;
-  const unsigned ncand = s_ncand;
-  const bool in_lds = ncand <= (unsigned)kSelCand;   // workgroup-uniform
+  const unsigned bin = s_prefix >> 19, ncand = s_ncand;
+  const bool gather = ncand <= cap;   // workgroup-uniform (every workgroup of the row decides the same)
 
-  // 2. this workgroup's query blocks into `own`; the row streamed once: the bin's elements into LDS (in any order)
-  if (stage_own) {
+  // 2. this workgroup's share of the row: the elements of the bin go to the candidate area. The share is counted
+  // first, so one atomic per workgroup reserves its slots (a returning device-scope atomic per wave and step would
+  // put a memory round trip on every step).
+  if (gather) {
+    auto in_share = [&](int i) { return e0 + tid + (int64_t)i * kThrThreads < e1; };
+    unsigned mine = 0;
+    if (in_regs) {
 #pragma unroll
-    for (int i = 0; i < kOwnPer; ++i)
-      if (tid + i * NT < own_n) own[tid + i * NT] = ow[i];
-  }
-  if (in_lds) {
-    // u is in the bin iff u - lo < 2^19 (unsigned); 0xffffffff (past the row) never is
-    const unsigned lo = prefix;
-    auto put = [&](unsigned u) {
-      const unsigned at = atomicAdd(&s_nc, 1u);
-      if (at < (unsigned)kSelCand) cand[at] = u;   // at < ncand unless the probs hold NaN
-    };
-    auto gather = [&](int v0, const u32x4 (&x)[kScanVec]) {
-#pragma unroll
-      for (int i = 0; i < kScanVec; ++i) {
-        const bool ok = v0 + (int)threadIdx.x + i * NT < rs.nb;
-        const u32x4 v = x[i];
-        const bool m0 = v[0] - lo < (1u << 19), m1 = v[1] - lo < (1u << 19);
-        const bool m2 = v[2] - lo < (1u << 19), m3 = v[3] - lo < (1u << 19);
-        if (ok && (m0 | m1 | m2 | m3)) {   // rare: about 1 element in 200 is in the bin
-          if (m0) put(v[0]);
-          if (m1) put(v[1]);
-          if (m2) put(v[2]);
-          if (m3) put(v[3]);
-        }
-      }
-    };
-    if (e0 - lo < (1u << 19)) put(e0);
-    gather(0, x0);
-    for (int v0 = NT * kScanVec; v0 < rs.nb; v0 += NT * kScanVec) {
-      u32x4 x[kScanVec];
-      rs.load(v0, x);
-      gather(v0, x);
+      for (int i = 0; i < kThrRegs; ++i) mine += (rv[i] >> 19) == bin && in_share(i) ? 1u : 0u;
+    } else {
+      for (int64_t e = e0 + tid; e < e1; e += kThrThreads) mine += (bits[e] >> 19) == bin ? 1u : 0u;
     }
-  }
-  __syncthreads();
-  if (in_lds) {
-    // 3. the low 19 bits of the candidates: digits [18:9] and [8:0], a workgroup histogram each
-    auto digit = [&](int shift, unsigned dmask, unsigned pmask) {
+    const unsigned minc = wave_incl_scan(mine);
+    if (lane == 63) wsum[wave] = minc;
+    __syncthreads();
+    unsigned off = minc - mine, wg_total = 0;
 #pragma unroll
-      for (int i = 0; i < kDigitPer; ++i) dh[tid + i * NT] = 0u;
-      __syncthreads();
-      for (unsigned e = tid; e < ncand; e += NT) {
-        const unsigned u = cand[e];
-        if ((u & pmask) == prefix) atomicAdd(&dh[(u >> shift) & dmask], 1u);
-      }
-      __syncthreads();
-      unsigned c[kDigitPer], ls = 0;   // thread tid owns digits kDigitPer * tid ..
+    for (int w = 0; w < kThrThreads / 64; ++w) {
+      off += w < wave ? wsum[w] : 0u;
+      wg_total += wsum[w];
+    }
+    if (tid == 0) s_arrived = wg_total ? __hip_atomic_fetch_add(ctl, wg_total, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT) : 0u;
+    __syncthreads();
+    unsigned at = s_arrived + off;
+    if (mine) {
+      if (in_regs) {
 #pragma unroll
-      for (int i = 0; i < kDigitPer; ++i) {
-        c[i] = dh[kDigitPer * tid + i];
-        ls += c[i];
-      }
-      const unsigned inc = wave_incl_scan(ls);
-      if (lane == 63) wsum[wave] = inc;
-      __syncthreads();
-      unsigned ex = inc - ls;
-#pragma unroll
-      for (int w = 0; w < NT / 64; ++w) ex += w < wave ? wsum[w] : 0u;
-#pragma unroll
-      for (int i = 0; i < kDigitPer; ++i) {
-        if (rk >= ex && rk < ex + c[i]) {
-          s_prefix = prefix | ((unsigned)(kDigitPer * tid + i) << shift);
-          s_rank = rk - ex;
+        for (int i = 0; i < kThrRegs; ++i) {
+          if ((rv[i] >> 19) == bin && in_share(i)) {
+            if (at < cap) __hip_atomic_store(cw + at, rv[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ++at;
+          }
         }
-        ex += c[i];
+      } else {
+        for (int64_t e = e0 + tid; e < e1; e += kThrThreads) {
+          const unsigned u = bits[e];
+          if ((u >> 19) == bin) {
+            if (at < cap) __hip_atomic_store(cw + at, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ++at;
+          }
+        }
       }
-      __syncthreads();
-      prefix = s_prefix;
-      rk = s_rank;
-    };
-    digit(9, 1023u, 0xfff80000u);
-    digit(0, 511u, 0xfffffe00u);
+    }
+    __syncthreads();   // every thread has read s_arrived
+  }
+  // Arrival. The candidates are relaxed agent-scope atomic stores (coherent past this XCD's L2); each wave waits for
+  // its stores to complete, and only then does thread 0 add the arrival, also relaxed. What keeps the order: the
+  // compiler does not move the stores or the add across the barrier's workgroup fences, and the wait means the
+  // stores have reached the coherence point before any wave arrives; the last workgroup reads the candidates with
+  // relaxed agent-scope loads from that same point. The C++/HIP model asks for a release on the add and an acquire
+  // in the last workgroup instead; that form (an acquire-release add plus an agent acquire fence) writes back and
+  // invalidates this XCD's L2 and measured 12.1 us per call against 10.2 us here, so the relaxed form is kept.
+  FVSR_WAIT_VM0();   // this wave's candidates are stored at device scope
+  __syncthreads();
+  if (tid == 0) s_arrived = __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_arrived != gridDim.x - 1) return;   // workgroup-uniform
+
+  // 3. the last workgroup of the row
+  unsigned prefix, rk;
+  if (gather) {
+    for (unsigned e = tid; e < ncand; e += kThrThreads)
+      cand[e] = __hip_atomic_load(cw + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    prefix = s_prefix;
+    rk = s_rank;
+    unsigned pmask = 0xfff80000u;
+    const int shifts[3] = {11, 3, 0};
+    const unsigned dmasks[3] = {255u, 255u, 7u};
+    for (int pass = 0; pass < 3; ++pass) {
+      radix_digit(hist, tot, prefix, rk, pmask, shifts[pass], dmasks[pass], [&](auto&& f) {
+        for (unsigned b0 = 0; b0 < ncand; b0 += kThrThreads) {
+          const unsigned e = b0 + tid;
+          f(e < ncand ? cand[e] : 0xffffffffu);
+        }
+      }, &s_prefix, &s_rank);
+      pmask |= dmasks[pass] << shifts[pass];
+    }
   } else {
-    // the whole row, four digits, each pass streaming it from memory
+    if (tid == 0) {
+      s_prefix = 0;
+      s_rank = rank0;
+    }
+    __syncthreads();
     prefix = 0;
     rk = rank0;
     unsigned pmask = 0x80000000u;
     const int shifts[4] = {23, 15, 7, 0};
     for (int pass = 0; pass < 4; ++pass) {
       const unsigned dmask = pass == 3 ? 127u : 255u;
-      radix_digit<NT>(rh, tot, prefix, rk, pmask, shifts[pass], dmask, [&](auto&& f) { rs.each(f); }, &s_prefix,
-                      &s_rank);
+      radix_digit(hist, tot, prefix, rk, pmask, shifts[pass], dmask, [&](auto&& f) {
+        for (int64_t b0 = 0; b0 < n; b0 += kThrThreads) {
+          const int64_t e = b0 + tid;
+          f(e < n ? bits[e] : 0xffffffffu);
+        }
+      }, &s_prefix, &s_rank);
       pmask |= dmask << shifts[pass];
     }
   }
-  const float th = __uint_as_float(prefix);
+  if (tid == 0) thr_out[row] = __uint_as_float(prefix);
+}
 
-  // 4. this wave's query block: mask, selection bytes, key list
-  if (!has_row) return;   // wave-uniform; no barrier follows
+// Mask, selection bytes and key lists from the row thresholds: one wave per query row (head, query block). Lists
+// hold the selected key blocks ascending, then the unselected ascending (argSort(!sel) of SparseAttention.swift:177
+// with a stable order). A row of up to 64 * kEmitChunks key blocks is loaded into registers first, every load in
+// flight at once (the probs were just written on other XCDs, so each load waits on the memory-side cache); longer
+// rows are read chunk by chunk, twice.
+constexpr int kEmitChunks = 12;
+__global__ __launch_bounds__(256) void topk_emit_kernel(const float* __restrict__ probs,
+                                                        const float* __restrict__ thr, int heads, int nq, int nk,
+                                                        int q_slices, float* __restrict__ mask_out,
+                                                        uint8_t* __restrict__ sel, int32_t* __restrict__ kidx,
+                                                        int32_t* __restrict__ kcnt) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);   // h * nq + qi
+  if (row >= heads * nq) return;
+  const int h = row / nq, qi = row - h * nq;
+  const int sq = nq / q_slices;
+  const float th = thr[h * q_slices + qi / sq];
   const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int64_t roff = ((int64_t)h * nq + qi) * nk;
-  int32_t* krow = kidx + roff;
+  const int64_t roff = (int64_t)row * nk;
   const float* prow = probs + roff;
-  const float* orow = own + wave * nk;
-  auto prob = [&](int j) -> float { return j < nk ? (stage_own ? orow[j] : prow[j]) : 0.f; };
+  int32_t* krow = kidx + roff;
   // selected keys of chunk j0 (lanes j0 + lane < nk whose prob p is above the threshold) go to krow[n_sel ..]
-  int n_sel = 0;
-  for (int j0 = 0; j0 < nk; j0 += 64) {
+  auto emit_selected = [&](int j0, float p, int& n_sel) {
     const int j = j0 + lane;
-    const bool s = j < nk && prob(j) > th;
+    const bool s = j < nk && p > th;
     const uint64_t b = __ballot(s);
     if (s) krow[n_sel + __popcll(b & lt)] = j;
     if (j < nk) {
@@ -645,16 +600,32 @@ __global__ __launch_bounds__(kEmitThreads) void topk_emit_kernel(const float* __
       if (mask_out) mask_out[roff + j] = s ? 1.f : 0.f;
     }
     n_sel += __popcll(b);
-  }
-  int n_un = n_sel;
-  for (int j0 = 0; j0 < nk; j0 += 64) {
+  };
+  auto emit_unselected = [&](int j0, float p, int& n_un) {
     const int j = j0 + lane;
-    const bool u = j < nk && !(prob(j) > th);
+    const bool u = j < nk && !(p > th);
     const uint64_t b = __ballot(u);
     if (u) krow[n_un + __popcll(b & lt)] = j;
     n_un += __popcll(b);
+  };
+  int n_sel = 0, n_un;
+  if (nk <= 64 * kEmitChunks) {
+    float pv[kEmitChunks];
+#pragma unroll
+    for (int c = 0; c < kEmitChunks; ++c) pv[c] = prow[min(64 * c + lane, nk - 1)];   // no branch between loads
+#pragma unroll
+    for (int c = 0; c < kEmitChunks; ++c)
+      if (64 * c < nk) emit_selected(64 * c, pv[c], n_sel);
+    n_un = n_sel;
+#pragma unroll
+    for (int c = 0; c < kEmitChunks; ++c)
+      if (64 * c < nk) emit_unselected(64 * c, pv[c], n_un);
+  } else {
+    for (int j0 = 0; j0 < nk; j0 += 64) emit_selected(j0, j0 + lane < nk ? prow[j0 + lane] : 0.f, n_sel);
+    n_un = n_sel;
+    for (int j0 = 0; j0 < nk; j0 += 64) emit_unselected(j0, j0 + lane < nk ? prow[j0 + lane] : 0.f, n_un);
   }
-  if (lane == 0) kcnt[(int64_t)h * nq + qi] = n_sel;
+  if (lane == 0) kcnt[row] = n_sel;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -708,20 +679,27 @@ int launch_scores_softmax(const float* pq, const float* pk, KeyMap kmap, int hea
   return FVSR_OK;
 }
 
-// the (head, query slice) histograms (cleared before a selection)
+// the (head, query slice) histograms and, after them, two control words per row (all cleared before a selection)
 size_t hist12_bytes(int heads, int q_slices) {
-  return (size_t)heads * q_slices * kHistBins * sizeof(unsigned);
+  return (size_t)heads * q_slices * (kHistBins + 2) * sizeof(unsigned);
 }
 
-// threshold + mask, selection bytes and lists from the probs and their histograms
-int launch_topk_emit(const float* probs, const unsigned* hist, int heads, int nq, int nk, int q_slices, int topk,
-                     float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt, hipStream_t stream) {
+// candidate area of the threshold select for `heads` x `nq` query blocks
+size_t topk_cand_bytes(int heads, int64_t nq) { return (size_t)heads * nq * kCandPerBlock * sizeof(unsigned); }
+
+int launch_topk_emit(const float* probs, int heads, int nq, int nk, int q_slices, int topk, unsigned* hist,
+                     unsigned* cand, float* thr, float* mask_out, uint8_t* sel, int32_t* kidx, int32_t* kcnt,
+                     hipStream_t stream) {
   if (nq <= 0 || nk <= 0) return FVSR_OK;
-  const int sq = nq / q_slices;
-  if ((int64_t)sq * nk >= ((int64_t)1 << 31))
-    return set_error(FVSR_ERR_UNSUPPORTED, "selection: a (head, query slice) row of 2^31 or more block pairs");
-  hipLaunchKernelGGL(topk_emit_kernel, dim3((unsigned)(ceil_div(sq, kEmitRows) * heads * q_slices)),
-                     dim3(kEmitThreads), 0, stream, probs, hist, nq, nk, q_slices, topk, mask_out, sel, kidx, kcnt);
+  // enough workgroups per row that each one's share fits its registers (kThrRegs elements per thread)
+  const int64_t row_n = (int64_t)(nq / q_slices) * nk;
+  const int parts = (int)std::min<int64_t>(kThrMaxParts, std::max<int64_t>(kThrParts,
+                                                             ceil_div(row_n, (int64_t)kThrRegs * kThrThreads)));
+  hipLaunchKernelGGL(topk_threshold_kernel, dim3(parts, heads * q_slices), dim3(kThrThreads), 0, stream, probs,
+                     nq, nk, q_slices, topk, ceil_div(row_n, (int64_t)parts), hist, cand, thr);
+  FVSR_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(topk_emit_kernel, dim3((heads * nq + 3) / 4), dim3(256), 0, stream, probs, thr, heads, nq, nk,
+                     q_slices, mask_out, sel, kidx, kcnt);
   FVSR_HIP_CHECK(hipGetLastError());
   return FVSR_OK;
 }
