@@ -425,8 +425,10 @@ def threshold_margin(probs: np.ndarray, seqlen: int, topk: int) -> float:
     flat = probs.reshape(heads * seqlen, (nq // seqlen) * nk)
     n = flat.shape[1]
     k = min(n - 1, topk)
+    if k <= 0:   # nothing is kept: the threshold is the row's max, with no neighbour above it to tie with
+        return math.inf
     srow = np.sort(flat, axis=1)
     thr = srow[:, n - 1 - k]
-    above = srow[:, n - k] if k > 0 else np.full(thr.shape, np.inf)
+    above = srow[:, n - k]
     gap = (above - thr) / np.maximum(above, 1e-38)
     return float(gap.min())

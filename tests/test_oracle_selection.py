@@ -131,6 +131,14 @@ def test_oracle_mask_matches_scalar_loops(structured):
     assert (per_row == topk).all()
 
 
+def test_oracle_margin_matches_scalar_loops(structured):
+    q, k, local, s, lq, lk, heads, q_slices, topk, bm, bp, margin = structured
+    assert O.threshold_margin(bp, q_slices, topk) == pytest.approx(margin, rel=1e-9)
+    # top-k 0 keeps nothing: no kept neighbour above the threshold, so no tie is possible
+    assert O.threshold_margin(bp, q_slices, 0) == math.inf
+    assert selection_bruteforce(q, k, heads, q_slices, s, local, 0, lq, lk)[2] == math.inf
+
+
 def test_oracle_pooling_matches_scalar_loops(structured):
     q, k, local, s, lq, lk, heads, *_ = structured
     np.testing.assert_allclose(O.pool_blocks(k, heads, lk), pooled_bruteforce(k, heads, lk), rtol=1e-5, atol=1e-6)
