@@ -138,6 +138,48 @@ def test_dit_block_matches_oracle(dev, heads, ffn, bh, bw, rng, ctx_len, chunks)
     ring.close()
 
 
+def test_chained_blocks_match_oracle(dev):
+    """Config 5's shape of the computation at small size: every chunk's tokens through block 0, its output through
+    block 1, then block 2 (random-init blocks, each with its own ring layer; the oracle keeps one window cache per
+    block), over the streaming schedule 2, 1, 1 slices. The blocks' errors compound, so the bar is the per-block one
+    times the depth: relative Frobenius error <= 1.5e-2 after the third block."""
+    heads, ffn, bh, bw, rng, ctx_len, depth = 2, 512, 3, 3, 3, 100, 3
+    r = np.random.default_rng(31)
+    c, s = heads * 128, bh * bw
+    local = L.local_block_mask(bh, bw, rng)
+    t_mod = L.to_bf16((r.standard_normal((6, c)) * 0.1).astype(np.float32))
+    tm = _bf(t_mod, dev)
+    ring = fvsr_lcsa.KVRing(depth, heads, bh, bw, capacity=4, kv_len=3, device=dev.index or 0)
+    Ws, blks, caches = [], [], []
+    for _ in range(depth):
+        W = _weights(r, c, ffn, heads)
+        ctx = L.to_bf16(r.standard_normal((ctx_len, c)).astype(np.float32))
+        W["cross_k"], W["cross_v"] = D.cross_kv(ctx, W["cross_k_weight"], W["cross_k_bias"], W["cross_v_weight"],
+                                                W["cross_v_bias"], W["cross_norm_k_weight"])
+        blk = fvsr_lcsa.DiTBlock({k: _bf(v, dev) for k, v in W.items() if k not in ("cross_k", "cross_v")}, heads)
+        blk.set_context(_bf(ctx, dev))
+        Ws.append(W)
+        blks.append(blk)
+        caches.append(L.KVWindowCache())
+    for n_new, t0 in [(2, 0), (1, 4), (1, 6)]:
+        f, h, w = 2 * n_new, 8 * bh, 8 * bw
+        x = L.to_bf16(r.standard_normal((f * h * w, c)).astype(np.float32))
+        nk = (ring.slices(0) + n_new) * s
+        topk = n_new * s * nk + 1   # above the pair count: keep every in-window block
+        xg = _bf(x, dev)
+        ref = x
+        for layer in range(depth):
+            print(f"chained blocks chunk n_new={n_new} t0={t0} block {layer}", flush=True)
+            blks[layer].forward(ring, layer, xg, tm, n_new, t0, local, topk, mode=fvsr_lcsa.ATTN_KERNEL)
+            ref, _ = D.block_forward(ref, Ws[layer], t_mod, caches[layer], f, h, w, heads, t0, local, topk)
+            ref = L.to_bf16(np.asarray(ref, dtype=np.float32))   # the next block reads bf16 tokens
+        torch.cuda.synchronize()
+        err = _rel(xg.float().cpu().numpy(), ref)
+        print(f"  rel err after {depth} blocks {err:.3e}", flush=True)
+        assert err < 1.5e-2
+    ring.close()
+
+
 def test_reserved_block_calls_allocate_nothing(dev):
     """fvsr_ctx_reserve_block sizes the hipBLASLt state, the block workspace and the select/attention workspace up
     front: block calls of at most the reserved size then leave both workspaces as they are (no hipFree / hipMalloc
