@@ -84,7 +84,7 @@ class FVSRError(RuntimeError):
 
 def load(path: str = LIB_PATH) -> C.CDLL:
     if not os.path.exists(path):
-        raise ImportError(f"libfvsr_lcsa is not built ({path} missing): run __graft_entry__.build() first")
+        raise ImportError(f"libfvsr_lcsa is not built ({path} missing): build it first with python mlx-flashvsr-swift_amd/build_lib.py")
     lib = C.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

@@ -1,6 +1,6 @@
 """CPU oracle for the dense parts of one FlashVSR DiT block around the LCSA layer call.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker the HIP path is compared against. Only `tests/`,
+TEST INFRASTRUCTURE ONLY: the HIP path's results are compared against this module's. Only `tests/`,
 `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it; the product path never does.
 
 It restates, in numpy, the streaming `blockForward` of the reference (xocialize/mlx-flashvsr-swift), with bfloat16

@@ -1,6 +1,6 @@
 """CPU oracle for FlashVSR's locality-constrained sparse attention (LCSA) hot path.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker the HIP path is compared against. Only `tests/`,
+TEST INFRASTRUCTURE ONLY: the HIP path's results are compared against this module's. Only `tests/`,
 `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it; the product path never does.
 
 It restates, in numpy, what the reference (xocialize/mlx-flashvsr-swift) computes on the path

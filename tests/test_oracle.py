@@ -1,4 +1,4 @@
-"""CPU checks that pin the oracle (oracle/lcsa.py) before it is trusted as the checker.
+"""CPU checks that pin the oracle (oracle/lcsa.py) before the GPU results are compared against it.
 
 Sources of truth, none of which is the oracle's own formula retyped:
   - the reference's structure KATs (Tests/FlashVSRMLXTests/FlashVSRStructureTests.swift:34-75), ported verbatim;

@@ -1,5 +1,5 @@
-"""CPU checks that pin the oracle's dense DiT-block pieces (oracle/dit.py; DiT.swift:317-381,491-551) before it is
-trusted as the checker.
+"""CPU checks that pin the oracle's dense DiT-block pieces (oracle/dit.py; DiT.swift:317-381,491-551) before the GPU
+results are compared against it.
 
 Sources of truth other than the oracle's own formulas: torch's CPU float32 routines (F.linear, F.gelu with
 approximate="tanh", F.layer_norm), float64 brute-force softmax attention, and closed forms (GELU(0) = 0 and

@@ -1,5 +1,5 @@
 """CPU checks that pin the oracle's projection epilogue (WanRMSNorm, RoPE tables, ropeApply, window partition;
-DiT.swift:34-47,52-107,111-118,496-506) before it is trusted as the checker.
+DiT.swift:34-47,52-107,111-118,496-506) before the GPU results are compared against it.
 
 Sources of truth other than the oracle's formulas: torch's bfloat16 conversion and float32 RMS norm
 (torch.nn.functional.rms_norm), complex multiplication in complex128, and closed forms (position 0 is the identity,
