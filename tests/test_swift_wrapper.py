@@ -95,3 +95,15 @@ def test_signature_table_matches_prototype_arity():
     for name, n in protos.items():
         argtypes = _abi.SIGNATURES[name][1]
         assert len(argtypes) == n, f"{name}: signature table has {len(argtypes)} arguments, the prototype {n}"
+
+
+def test_every_constant_the_wrapper_names_is_declared():
+    """The enumerators the wrapper passes (FVSR_DTYPE_*, FVSR_ATTN_*, FVSR_LAYOUT_*) exist in the header, so the
+    imported Clang module provides them."""
+    header = open(HEADER).read()
+    declared = set(re.findall(r"\b(FVSR_[A-Z0-9_]+)\s*=", header)) | set(re.findall(r"#define\s+(FVSR_[A-Z0-9_]+)", header))
+    text = "\n".join(line.split("//")[0] for line in open(SWIFT).read().splitlines())
+    used = set(re.findall(r"\b(FVSR_[A-Z0-9_]+)\b", text))
+    assert used, "the wrapper names no FVSR_ constant"
+    assert used <= declared, f"not declared in include/fvsr_lcsa.h: {sorted(used - declared)}"
+
