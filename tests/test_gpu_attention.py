@@ -172,6 +172,43 @@ def test_list_order_does_not_change_the_result(dev):
     assert O.compare(_np(a), _np(b))["rel"] <= 1e-6
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rows_whose_exponentials_all_underflow_are_redone(dev, dtype):
+    """The walk's exact redo (a row-max pass, then attention with that max): a row whose first listed block lies
+    outside [0, nk) gets the reference 0 from that all-masked first tile, and when every real score sits ~196 below
+    it (log2 units) all of its exponentials underflow to 0. Such rows must still give the softmax over their valid
+    blocks, as the oracle computes it (out-of-range entries take no part). Head 1's rows list valid blocks first and
+    share the launch."""
+    heads, lq, lk = 2, 256, 4 * 128 - 40
+    nk = 4
+    gen = torch.Generator().manual_seed(23)
+    q = torch.randn((lq, heads * 128), generator=gen)
+    k = torch.randn((lk, heads * 128), generator=gen)
+    v = torch.randn((lk, heads * 128), generator=gen)
+    q[:, :128] = 4.0 + 0.25 * torch.randn((lq, 128), generator=gen)     # head 0: q.k ~ -1536 +- 14
+    k[:, :128] = -3.0 + 0.25 * torch.randn((lk, 128), generator=gen)
+    q, k, v = (t.to(dtype) for t in (q, k, v))
+    lists = {(0, 0): [nk + 5, 0, 3], (0, 1): [-3, 1, 2, 3], (1, 0): [0, 1], (1, 1): [3, 2]}
+    kidx = np.zeros((heads, 2, nk), dtype=np.int32)
+    kcnt = np.zeros((heads, 2), dtype=np.int32)
+    mask = np.zeros((heads, 2, nk), dtype=np.float32)
+    for (h, i), l in lists.items():
+        kidx[h, i, :len(l)] = l
+        kcnt[h, i] = len(l)
+        for j in l:
+            if 0 <= j < nk:
+                mask[h, i, j] = 1.0
+    o = fvsr_lcsa.block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(kidx).to(dev),
+                                         torch.from_numpy(kcnt).to(dev), heads)
+    torch.cuda.synchronize()
+    ref = O.block_masked_attention(_np(q), _np(k), _np(v), mask, heads)
+    assert np.abs(ref[:, :128]).max() > 0.1                      # head 0 is a real softmax, not zeros
+    rel = _rel(o, ref)
+    # fp32 (its own kernel, no redo needed): head 0's scores are ~1.5e3 in magnitude, so their fp32 rounding (a few
+    # 1e-4 absolute) moves the weights by ~1e-4 relative against the float64 oracle
+    assert rel <= (BF16_REL if dtype == torch.bfloat16 else 1e-4), rel
+
+
 def test_c1_fp32_parity(dev):
     """512x512 fp32 workload: Lq 2048, Lk 6144, 12 heads, the oracle's own mask; rel <= 1e-5."""
     wl = synth.WORKLOADS["lcsa_512x512_fp32"]
