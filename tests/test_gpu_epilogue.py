@@ -37,7 +37,9 @@ def _close_pairs(got, ref):
     return float((got == ref).mean())
 
 
-@pytest.mark.parametrize("f,h,w,heads,t0", [(2, 16, 24, 12, 5), (4, 8, 8, 4, 0), (2, 72, 120, 12, 8)])
+# heads 4, 8, 12, 16, 20: the kernel's register sizing (16-byte vectors per lane) 1, 2, 3, 4 and 5
+@pytest.mark.parametrize("f,h,w,heads,t0", [(2, 16, 24, 12, 5), (4, 8, 8, 4, 0), (2, 72, 120, 12, 8),
+                                            (2, 8, 8, 8, 1), (2, 8, 16, 16, 2), (2, 8, 8, 20, 0)])
 def test_epilogue_bf16_vs_oracle(dev, f, h, w, heads, t0):
     q, k, v, wq, wk = _inputs(f, h, w, heads, torch.bfloat16, seed=f * 1000 + t0)
     qo, ko, vo = fvsr_lcsa.qkv_epilogue(q.to(dev), k.to(dev), v.to(dev), f, h, w, heads, t0, wq.to(dev), wk.to(dev))
@@ -49,8 +51,9 @@ def test_epilogue_bf16_vs_oracle(dev, f, h, w, heads, t0):
     assert _close_pairs(ko, rk) >= 0.99
 
 
-def test_epilogue_fp32_vs_oracle(dev):
-    f, h, w, heads, t0 = 2, 16, 16, 12, 3
+@pytest.mark.parametrize("heads", [12, 4])   # 16-byte vectors per lane: 6 and 2
+def test_epilogue_fp32_vs_oracle(dev, heads):
+    f, h, w, t0 = 2, 16, 16, 3
     q, k, v, wq, wk = _inputs(f, h, w, heads, torch.float32, seed=7)
     qo, ko, vo = fvsr_lcsa.qkv_epilogue(q.to(dev), k.to(dev), v.to(dev), f, h, w, heads, t0, wq.to(dev), wk.to(dev))
     rq, rk, rv = O.qkv_epilogue(q.numpy(), k.numpy(), v.numpy(), f, h, w, heads, t0, wq.numpy(), wk.numpy(),
