@@ -84,7 +84,10 @@ def test_select_and_attention_over_ring_equal_plain(dev, dtype):
         ring.evict(0)
 
 
-def test_layer_call_equals_manual_sequence(dev):
+# AUTO with top-k 3 n s keeps an expected (3 n s + 1) / (s nk) of the pairs: over 0.45 in chunk 0 (dense walk), under
+# it afterwards (the kernel walk); both walks give the kernel's result bit for bit (DiT.swift:517-522)
+@pytest.mark.parametrize("mode", ["kernel", "auto"])
+def test_layer_call_equals_manual_sequence(dev, mode):
     heads, bh, bw, r = 2, 2, 2, 3
     s = bh * bw
     local = O.local_block_mask(bh, bw, r)
@@ -92,11 +95,12 @@ def test_layer_call_equals_manual_sequence(dev):
     ring_a = fvsr_lcsa.KVRing(1, heads, bh, bw, 4, 3, dtype)
     ring_b = fvsr_lcsa.KVRing(1, heads, bh, bw, 4, 3, dtype)
     gen = torch.Generator().manual_seed(21)
+    call_mode = fvsr_lcsa.ATTN_KERNEL if mode == "kernel" else fvsr_lcsa.ATTN_AUTO
     for n, kn, vn in _chunks(heads, bh, bw, dtype, schedule=(3, 1, 1, 1)):
         q = torch.randn((n * s * 128, heads * 128), generator=gen).to(dtype).to(dev)
         kd, vd = kn.to(dev), vn.to(dev)
         topk = 3 * n * s
-        o_a, m_a, p_a = ring_a.layer_call(0, q, kd, vd, n, n, local, topk, mode=fvsr_lcsa.ATTN_KERNEL,
+        o_a, m_a, p_a = ring_a.layer_call(0, q, kd, vd, n, n, local, topk, mode=call_mode,
                                           want_mask=True, want_probs=True)
         ring_b.append(0, kd, vd, n)
         m_b, p_b, ki, kc = ring_b.select(0, q, n, local, topk)
